@@ -1,0 +1,167 @@
+/*
+ * dsa_amd.h -- C ABI of the MI355X (gfx950) DeepSeek-sparse-attention decode path.
+ *
+ * Library: nanoengine_amd/libdsa_amd.so (hipcc, --offload-arch=gfx950).
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers; sizes and strides are in ELEMENTS of the
+ *     pointed-to type unless the name ends in `_bytes`.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Kernels are launched asynchronously on it; nothing synchronises the
+ *     host, nothing allocates, so every call is capturable in a HIP graph.
+ *   - The caller owns and allocates every output and workspace.
+ *   - Return value: 0 on success, otherwise a dsa status code
+ *     (1 invalid argument, 2 unsupported shape, 3 launch failure,
+ *     4 workspace too small); dsa_last_error() then describes the failure.
+ *
+ * Citations name the reference interface (nano-infra/NanoEngine, package
+ * dlengine) that each entry point replaces.
+ */
+#ifndef DSA_AMD_H_
+#define DSA_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define DSA_API __attribute__((visibility("default")))
+#else
+#define DSA_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version (major*10000 + minor*100 + patch). */
+DSA_API int dsa_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+DSA_API const char* dsa_last_error(void);
+
+/* Compute units of `device`.
+ * Replaces deep_gemm.get_num_sms() (called at
+ * dlengine/runtime/layers/backends/dsa/indexer/lightning.py:633). */
+DSA_API int dsa_num_cus(int device);
+
+/* Largest score-row length the top-k kernels accept (positions per row). */
+DSA_API int dsa_topk_max_len(void);
+
+/* Indexer work schedule. Writes `batch + 1` int32 values to
+ * `schedule_out`: the exclusive prefix sum of per-sequence page counts
+ * ceil(max_j context_lens[b, j] / page_size). The logits kernel does not need
+ * it (its grid covers every page with early exit), but the call exists so the
+ * caller's once-per-forward schedule step stays in place.
+ * Replaces deep_gemm.get_paged_mqa_logits_metadata(context_lens, page_size,
+ * num_sms) (lightning.py:668-676; built once per forward at
+ * dlengine/runtime/models/deepseek_v2/deepseek_v2.py:807-840). */
+DSA_API int dsa_indexer_schedule(const int32_t* context_lens, int batch, int next_n,
+                         int page_size, int32_t* schedule_out, void* stream);
+
+/* fp8 lightning-indexer logits over the paged indexer cache.
+ *   q_fp8        [batch, next_n, num_heads=64, head_dim=128] e4m3fn bytes, contiguous
+ *   kv_cache     [num_pages, page_size*132] bytes; page = [page_size x 128 fp8][page_size x f32 scale]
+ *   weights      [batch*next_n, num_heads] f32 (q scale and softmax scale folded in)
+ *   context_lens [batch, next_n] int32 (per-query causal length)
+ *   block_tables [batch, >= ceil(max_ctx/page_size)] int32, row stride `block_table_stride`
+ *   logits       [batch*next_n, max_context_len] f32, row stride `logits_stride`
+ * logits[b*n+j, t] = sum_h weights[b*n+j, h] * relu(q[b,j,h,:] . k[t,:]) * scale[t]
+ * for t < context_lens[b, j]; positions past the context inside the last page
+ * are written as -inf, later positions are not written.
+ * next_n in {1, 2}; page_size == 64; num_heads == 64; head_dim == 128.
+ * Replaces deep_gemm.fp8_paged_mqa_logits(q_fp8, kv_cache, weights,
+ * context_lens, block_tables, schedule_meta, max_context_len,
+ * clean_logits=False) (lightning.py:1395-1406). */
+DSA_API int dsa_indexer_logits(const uint8_t* q_fp8, const uint8_t* kv_cache,
+                       const float* weights, const int32_t* context_lens,
+                       const int32_t* block_tables, int64_t block_table_stride,
+                       int batch, int next_n, int num_heads, int head_dim,
+                       int page_size, int64_t max_context_len,
+                       float* logits, int64_t logits_stride, void* stream);
+
+/* Exact top-k selection with page-table translation.
+ *   scores          [batch, >= seq_lens[b]] f32, row stride `score_stride`
+ *   seq_lens        [batch] int32
+ *   page_table      [batch, ...] int32, row stride `page_table_stride`, or NULL:
+ *                   then out_page receives the raw positions (no translation)
+ *   out_page        [batch, top_k] int32, contiguous
+ *   out_raw         [batch, top_k] int32 or NULL
+ * Row b selects the top_k largest scores among positions [0, seq_lens[b])
+ * (ties: lowest positions; NaN ranks as -inf), writes them in ascending
+ * position order as raw positions and as slots
+ * (page_table[p >> log2(page_size)] << log2(page_size)) | (p & (page_size-1)),
+ * then pads with -1. seq_lens[b] <= top_k emits 0..seq_lens[b]-1.
+ * top_k in {512, 2048}; page_size a power of two;
+ * row length <= dsa_topk_max_len(); `max_len` bounds seq_lens (the score width).
+ * Replaces topk_transform(scores, seq_lens, page_tables, out_page_indices,
+ * page_size, top_k, out_raw_indices)
+ * (dlengine/runtime/kernel/jit/sgl/deepseek_v4.py:324-367,
+ *  kernel csrc/deepseek_v4/topk.cuh:249-287, host TopKKernel::transform :336-394). */
+DSA_API int dsa_topk_transform(const float* scores, int64_t score_stride,
+                       const int32_t* seq_lens, const int32_t* page_table,
+                       int64_t page_table_stride, int32_t* out_page,
+                       int32_t* out_raw, int batch, int64_t max_len,
+                       int page_size, int top_k, void* stream);
+
+/* Ragged exact top-k: row b selects among scores[b, row_starts[b] +
+ * [0, seq_lens[b])] and writes position + offsets[b], ascending, padded -1.
+ * top_k == 2048. Exact (the reference's bounded candidate buffer allows a few
+ * differences; this kernel has none).
+ * Replaces topk_transform_ragged(scores, seq_lens, row_starts, offsets,
+ * out_indices, top_k) (deepseek_v4.py:370-388, topk.cuh:289-316). */
+DSA_API int dsa_topk_transform_ragged(const float* scores, int64_t score_stride,
+                              const int32_t* seq_lens, const int32_t* row_starts,
+                              const int32_t* offsets, int32_t* out,
+                              int batch, int64_t max_len, int top_k, void* stream);
+
+/* Logical token positions -> physical cache slots.
+ *   topk_indices [rows, topk] int32, row stride `topk_stride` (-1 = padding)
+ *   block_table  [rows / rows_per_table, table_width] int32, row stride `bt_stride`
+ *   out          [rows, topk] int32, contiguous
+ * out = block_table[r / rows_per_table, i / block_size] * block_size + i % block_size,
+ * -1 kept; a position whose page lies beyond table_width also maps to -1.
+ * rows_per_table = next_n expresses block_tables.repeat_interleave(next_n)
+ * (deepseek_v2.py:1940-1946) without materialising it.
+ * Replaces topk_indices_to_physical(topk_indices, block_table, block_size)
+ * (dlengine/runtime/layers/backends/attention/mla_utils.py:237-272). */
+DSA_API int dsa_topk_to_physical(const int32_t* topk_indices, int64_t topk_stride,
+                         const int32_t* block_table, int64_t bt_stride,
+                         int table_width, int rows, int topk, int rows_per_table,
+                         int block_size, int32_t* out, void* stream);
+
+/* Split count the sparse MLA decode uses for this shape (1 = no workspace). */
+DSA_API int dsa_sparse_mla_num_splits(int num_tokens, int num_heads, int topk, int num_cus);
+
+/* Workspace bytes dsa_sparse_mla_decode needs for `num_splits`. */
+DSA_API size_t dsa_sparse_mla_workspace_bytes(int num_tokens, int num_heads, int num_splits);
+
+/* Sparse MLA decode over the packed fp8 MLA cache.
+ *   q        [num_tokens, num_heads, 576] bf16, row stride q_token_stride,
+ *            head stride q_head_stride (elements; last dim contiguous)
+ *   kv_cache block b row r at kv_cache + b*kv_block_stride_bytes + r*656:
+ *            [512 e4m3fn][4 x f32 tile scale][64 x bf16 rope]
+ *   indices  [num_tokens, topk] int32 physical slots (block*kv_block_size+row),
+ *            row stride idx_stride, -1 = skip
+ *   out      [num_tokens, num_heads, 512] bf16, contiguous
+ *   lse      [num_tokens, num_heads] f32 natural-log LSE, contiguous (may be NULL)
+ * o = softmax(sm_scale * q . kv) @ kv[:, :512] over valid indices; a token with
+ * no valid index yields o = 0 and lse = -inf.
+ * num_heads % 16 == 0; topk % 64 == 0; num_splits in [1, topk/64] with
+ * workspace >= dsa_sparse_mla_workspace_bytes(...) when num_splits > 1
+ * (num_splits <= 0 picks dsa_sparse_mla_num_splits for this device).
+ * Replaces flash_mla.flash_mla_with_kvcache(q, k_cache, None, None,
+ * head_dim_v=512, sched_meta, None, softmax_scale, causal=False,
+ * is_fp8_kvcache=True, indices=...) as called by FlashMlaAttention.forward
+ * (dlengine/runtime/layers/backends/mla/flash_mla.py:76-99). */
+DSA_API int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                          const uint8_t* kv_cache, int64_t kv_block_stride_bytes,
+                          int kv_block_size, const int32_t* indices, int64_t idx_stride,
+                          int num_tokens, int num_heads, int topk, float sm_scale,
+                          void* out, float* lse, int num_splits,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* DSA_AMD_H_ */

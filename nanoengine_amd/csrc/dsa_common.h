@@ -1,0 +1,77 @@
+// Shared device helpers for the DSA decode kernels (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+namespace dsa {
+
+// Status codes shared by every C entry point (0 = success).
+enum Status : int {
+  kOk = 0,
+  kInvalidArgument = 1,
+  kUnsupported = 2,
+  kLaunchFailed = 3,
+  kWorkspaceTooSmall = 4,
+};
+
+// Records a human-readable message for dsa_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// Monotone uint32 key of a float: larger float -> larger key. NaN ranks as -inf.
+__device__ __forceinline__ uint32_t order_key(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (x != x) u = 0xff800000u;  // -inf
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Two OCP e4m3fn bytes (selected by `hi`: bytes 0-1 or 2-3 of w) -> two floats.
+__device__ __forceinline__ v2f fp8x2_to_f32(uint32_t w, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true)
+            : __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+}
+
+// Pack the bf16 truncations of two floats (lo in bits 0-15). Exact for values
+// that are already bf16-representable, such as fp8 times a power of two.
+__device__ __forceinline__ uint32_t pack_bf16_trunc(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// Round-to-nearest-even float -> bf16 bits.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (x != x) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+  return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+}
+
+// Dequantise 16 fp8 bytes (v4i) with a power-of-two scale into 16 bf16 (two v4i).
+__device__ __forceinline__ void dequant16_fp8_bf16(v4i raw, float scale, v4i& lo, v4i& hi) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    v2f a = fp8x2_to_f32((uint32_t)raw[w], false);
+    v2f b = fp8x2_to_f32((uint32_t)raw[w], true);
+    uint32_t p0 = pack_bf16_trunc(a.x * scale, a.y * scale);
+    uint32_t p1 = pack_bf16_trunc(b.x * scale, b.y * scale);
+    if (w < 2) { lo[2 * w] = (int)p0; lo[2 * w + 1] = (int)p1; }
+    else       { hi[2 * (w - 2)] = (int)p0; hi[2 * (w - 2) + 1] = (int)p1; }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+}  // namespace dsa

@@ -1,0 +1,401 @@
+// Sparse MLA decode over the packed fp8 MLA cache, for gfx950.
+//
+// For each query token t and head h:
+//   s_i = sm_scale * q[t,h,:576] . kv(idx_i)[:576]     (valid idx_i only)
+//   o   = softmax(s) @ kv(idx)[:, :512],  lse = log(sum_i exp(s_i))
+// where kv(slot) is a 656-byte row [512 e4m3fn][4 x f32 tile scale][64 bf16].
+//
+// Workgroup = 4 waves = 64 heads of one token over one key split. Per block of
+// 64 selected rows:
+//   load   : lane = row; wave w gathers tile w of the 64 rows (8 x 16 B fp8 +
+//            its f32 scale) and two 16 B rope chunks, one block ahead of use,
+//            so HBM latency hides behind the previous block's MFMAs;
+//   stage  : rows are dequantised in registers (fp8 * 2^k is exact in bf16)
+//            and written to LDS twice: row-major Kb[64][576] for Q.K^T and
+//            transposed Vt[512][64] for P.V;
+//   QK     : wave w computes S^T[64 keys x 16 heads] with
+//            v_mfma_f32_16x16x32_bf16, A = Kb rows from LDS, B = its 16 query
+//            heads held in registers for the whole kernel (18 x 8 bf16);
+//   softmax: online (running max / sum in the exp2 domain), the max reduced
+//            across the four 16-lane groups with two shuffles;
+//   PV     : O^T[512 x 16 heads] += Vt . P^T, with P^T taken directly from the
+//            QK accumulators (no LDS round trip: the MFMA C layout of two
+//            16-key tiles is a key permutation of the B layout, and Vt is read
+//            with the same permutation).
+// Splits over the key list (for small batches) write normalised partial
+// outputs and LSEs to a caller-provided workspace; a combine kernel merges
+// them with the LSE rule of merge_attention_states.
+#include <cmath>
+
+#include "dsa_common.h"
+#include "../../include/dsa_amd.h"
+
+namespace dsa {
+
+constexpr int kMlaThreads = 256;
+constexpr int kMlaHeadsPerWG = 64;
+constexpr int kMlaKeys = 64;           // rows per block
+constexpr int kMlaRowBytes = 656;
+constexpr int kMlaDqk = 576;
+constexpr int kMlaDv = 512;
+constexpr int kKbPitch = kMlaDqk * 2 + 16;  // bytes per staged key row
+constexpr int kVtPitch = kMlaKeys * 2 + 16; // bytes per staged value column
+constexpr int kKbBytes = kMlaKeys * kKbPitch;
+constexpr int kVtBytes = kMlaDv * kVtPitch;
+constexpr size_t kMlaSmemBytes = (size_t)kKbBytes + kVtBytes;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct MlaParams {
+  const uint16_t* q;
+  int64_t q_tok_stride, q_head_stride;
+  const uint8_t* kv;
+  int64_t kv_blk_stride;
+  int kv_block_size;
+  const int32_t* idx;
+  int64_t idx_stride;
+  int T, H, topk, splits, head_groups;
+  float scale_log2;
+  uint16_t* out;
+  float* lse;
+  float* ws_o;    // [splits, T, H, 512] (splits > 1)
+  float* ws_lse;  // [splits, T, H]
+};
+
+struct RowRegs {
+  v4i nope[8];   // this wave's 128-dim tile of the lane's row
+  v4i rope[2];   // rope chunks 2w, 2w+1
+  float scale;
+};
+
+__device__ __forceinline__ void load_rows(RowRegs& rr, const MlaParams& P, int t, int key0, int lane,
+                                          int wave, bool& valid) {
+  const int32_t slot = P.idx[(int64_t)t * P.idx_stride + key0 + lane];
+  valid = slot >= 0;
+  if (valid) {
+    const uint8_t* row = P.kv + (int64_t)(slot / P.kv_block_size) * P.kv_blk_stride +
+                         (int64_t)(slot % P.kv_block_size) * kMlaRowBytes;
+    const v4i* nope = reinterpret_cast<const v4i*>(row + wave * 128);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rr.nope[i] = nope[i];
+    rr.scale = reinterpret_cast<const float*>(row + 512)[wave];
+    const v4i* rope = reinterpret_cast<const v4i*>(row + 528 + wave * 32);
+    rr.rope[0] = rope[0];
+    rr.rope[1] = rope[1];
+  } else {
+    const v4i z = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rr.nope[i] = z;
+    rr.rope[0] = z;
+    rr.rope[1] = z;
+    rr.scale = 0.f;
+  }
+}
+
+__device__ __forceinline__ void stage_rows(const RowRegs& rr, uint8_t* kb, uint8_t* vt, int lane, int wave) {
+  uint8_t* krow = kb + lane * kKbPitch;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = wave * 8 + i;  // 16-dim chunk index, dims 16c .. 16c+15
+    v4i lo, hi;
+    dequant16_fp8_bf16(rr.nope[i], rr.scale, lo, hi);
+    *reinterpret_cast<v4i*>(krow + c * 32) = lo;
+    *reinterpret_cast<v4i*>(krow + c * 32 + 16) = hi;
+    uint16_t* vcol = reinterpret_cast<uint16_t*>(vt + (c * 16) * kVtPitch) + lane;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vcol[(2 * e) * (kVtPitch / 2)] = (uint16_t)lo[e];
+      vcol[(2 * e + 1) * (kVtPitch / 2)] = (uint16_t)((uint32_t)lo[e] >> 16);
+      vcol[(8 + 2 * e) * (kVtPitch / 2)] = (uint16_t)hi[e];
+      vcol[(8 + 2 * e + 1) * (kVtPitch / 2)] = (uint16_t)((uint32_t)hi[e] >> 16);
+    }
+  }
+  *reinterpret_cast<v4i*>(krow + 1024 + wave * 32) = rr.rope[0];
+  *reinterpret_cast<v4i*>(krow + 1024 + wave * 32 + 16) = rr.rope[1];
+}
+
+__device__ __forceinline__ v8bf as_v8bf(v4i x) { return __builtin_bit_cast(v8bf, x); }
+
+__global__ void __launch_bounds__(kMlaThreads)
+sparse_mla_kernel(const MlaParams P) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint8_t* kb = smem;
+  uint8_t* vt = smem + kKbBytes;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+
+  // XCD-aware order: consecutive logical work items (the head groups and
+  // splits of one token) land on the same XCD and share its L2.
+  const int nwg = gridDim.x;
+  int work = blockIdx.x;
+  if ((nwg & 7) == 0) work = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+  const int per_tok = P.head_groups * P.splits;
+  const int t = work / per_tok;
+  const int rem = work % per_tok;
+  const int hg = rem / P.splits;
+  const int split = rem % P.splits;
+  const int chunk = P.topk / P.splits;
+  const int key_begin = split * chunk;
+
+  const int h0 = hg * kMlaHeadsPerWG + wave * 16;
+  const bool active = h0 < P.H;
+
+  // Query heads as B operands: head h0 + lane%16, dims ks*32 + g*8 .. +8.
+  v4i qb[18];
+  if (active) {
+    const uint16_t* qh = P.q + (int64_t)t * P.q_tok_stride + (int64_t)(h0 + c16) * P.q_head_stride + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < 18; ++ks) qb[ks] = *reinterpret_cast<const v4i*>(qh + ks * 32);
+  }
+
+  v4f acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+  float m_run = -__builtin_inff();
+  float l_run = 0.f;
+
+  RowRegs rr;
+  bool valid;
+  load_rows(rr, P, t, key_begin, lane, wave, valid);
+
+  for (int key0 = key_begin; key0 < key_begin + chunk; key0 += kMlaKeys) {
+    const uint64_t vmask = __ballot(valid);
+    __syncthreads();  // previous block's LDS reads are done
+    stage_rows(rr, kb, vt, lane, wave);
+    __syncthreads();
+    if (key0 + kMlaKeys < key_begin + chunk) load_rows(rr, P, t, key0 + kMlaKeys, lane, wave, valid);
+    if (!active || vmask == 0) continue;
+
+    // S^T tiles: s[kt][r] = score(key kt*16 + g*4 + r, head lane%16)
+    v4f s[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      v4f c = {0.f, 0.f, 0.f, 0.f};
+      const uint8_t* arow = kb + (kt * 16 + c16) * kKbPitch + g * 16;
+#pragma unroll
+      for (int ks = 0; ks < 18; ++ks) {
+        const v4i a = *reinterpret_cast<const v4i*>(arow + ks * 64);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a), as_v8bf(qb[ks]), c, 0, 0, 0);
+      }
+      s[kt] = c;
+    }
+
+    float mloc = -__builtin_inff();
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kt * 16 + g * 4 + r;
+        const float x = ((vmask >> key) & 1ull) ? s[kt][r] * P.scale_log2 : -__builtin_inff();
+        s[kt][r] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = fmaxf(mloc, shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+    const float m_new = fmaxf(m_run, mloc);  // finite: vmask != 0
+    const float alpha = exp2f(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = exp2f(s[kt][r] - m_new);
+        s[kt][r] = pv;
+        psum += pv;
+      }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[i] *= alpha;
+    }
+
+    // P^T operands for the two 32-key steps.
+    v4i pb[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      pb[kk][0] = (int)pack_bf16_rne(s[2 * kk][0], s[2 * kk][1]);
+      pb[kk][1] = (int)pack_bf16_rne(s[2 * kk][2], s[2 * kk][3]);
+      pb[kk][2] = (int)pack_bf16_rne(s[2 * kk + 1][0], s[2 * kk + 1][1]);
+      pb[kk][3] = (int)pack_bf16_rne(s[2 * kk + 1][2], s[2 * kk + 1][3]);
+    }
+
+#pragma unroll
+    for (int dt = 0; dt < 32; ++dt) {
+      const uint8_t* vrow = vt + (dt * 16 + c16) * kVtPitch + g * 8;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + kk * 64);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + kk * 64 + 32);
+        const v4i a = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a), as_v8bf(pb[kk]), acc[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  if (!active) return;
+  l_run += shfl_xor(l_run, 16);
+  l_run += shfl_xor(l_run, 32);
+  const int h = h0 + c16;
+  const bool any = l_run > 0.f;
+  const float inv = any ? 1.f / l_run : 0.f;
+  const float lse = any ? (m_run + log2f(l_run)) * kLn2 : -__builtin_inff();
+
+  if (P.splits == 1) {
+    uint16_t* o = P.out + ((int64_t)t * P.H + h) * kMlaDv + g * 4;
+#pragma unroll
+    for (int dt = 0; dt < 32; ++dt) {
+      uint2 v;
+      v.x = pack_bf16_rne(acc[dt][0] * inv, acc[dt][1] * inv);
+      v.y = pack_bf16_rne(acc[dt][2] * inv, acc[dt][3] * inv);
+      *reinterpret_cast<uint2*>(o + dt * 16) = v;
+    }
+    if (g == 0 && P.lse) P.lse[(int64_t)t * P.H + h] = lse;
+  } else {
+    const int64_t row = ((int64_t)split * P.T + t) * P.H + h;
+    float* o = P.ws_o + row * kMlaDv + g * 4;
+#pragma unroll
+    for (int dt = 0; dt < 32; ++dt) {
+      v4f v = acc[dt] * inv;
+      *reinterpret_cast<v4f*>(o + dt * 16) = v;
+    }
+    if (g == 0) P.ws_lse[row] = lse;
+  }
+}
+
+// One 64-thread workgroup per (token, head): merge the split partials.
+__global__ void __launch_bounds__(64)
+sparse_mla_combine_kernel(const float* __restrict__ ws_o, const float* __restrict__ ws_lse, int T, int H,
+                          int splits, uint16_t* __restrict__ out, float* __restrict__ lse_out) {
+  const int th = blockIdx.x;
+  const int64_t stride = (int64_t)T * H;
+  float m = -__builtin_inff();
+  for (int s = 0; s < splits; ++s) m = fmaxf(m, ws_lse[s * stride + th]);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.f;
+  if (m != -__builtin_inff()) {
+    for (int s = 0; s < splits; ++s) {
+      const float l = ws_lse[s * stride + th];
+      const float w = __expf(l - m);
+      wsum += w;
+      const v4f* src = reinterpret_cast<const v4f*>(ws_o + (s * stride + th) * kMlaDv + threadIdx.x * 8);
+      const v4f a = src[0], b = src[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[e] = fmaf(w, a[e], acc[e]);
+        acc[4 + e] = fmaf(w, b[e], acc[4 + e]);
+      }
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  v4i v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (int)pack_bf16_rne(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+  *reinterpret_cast<v4i*>(out + (int64_t)th * kMlaDv + threadIdx.x * 8) = v;
+  if (threadIdx.x == 0 && lse_out) lse_out[th] = wsum > 0.f ? m + logf(wsum) : -__builtin_inff();
+}
+
+}  // namespace dsa
+
+extern "C" {
+
+int dsa_sparse_mla_num_splits(int num_tokens, int num_heads, int topk, int num_cus) {
+  if (num_tokens <= 0 || num_heads <= 0 || topk <= 0) return 1;
+  if (num_cus <= 0) num_cus = 256;
+  const int groups = (num_heads + dsa::kMlaHeadsPerWG - 1) / dsa::kMlaHeadsPerWG;
+  const int64_t base = (int64_t)num_tokens * groups;
+  int splits = 1;
+  const int max_splits = topk / dsa::kMlaKeys;
+  // grow until the grid covers the CUs once; splits must divide topk into 64-row blocks
+  while (base * splits < num_cus && splits * 2 <= max_splits && (topk / (splits * 2)) % dsa::kMlaKeys == 0)
+    splits *= 2;
+  return splits;
+}
+
+size_t dsa_sparse_mla_workspace_bytes(int num_tokens, int num_heads, int num_splits) {
+  if (num_splits <= 1 || num_tokens <= 0 || num_heads <= 0) return 0;
+  const size_t rows = (size_t)num_splits * num_tokens * num_heads;
+  return rows * dsa::kMlaDv * sizeof(float) + rows * sizeof(float);
+}
+
+int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                          const uint8_t* kv_cache, int64_t kv_block_stride_bytes, int kv_block_size,
+                          const int32_t* indices, int64_t idx_stride, int num_tokens, int num_heads,
+                          int topk, float sm_scale, void* out, float* lse, int num_splits, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  using namespace dsa;
+  if (num_tokens < 0 || num_heads <= 0 || (num_heads % 16) != 0)
+    return set_error(kUnsupported, "sparse_mla: num_heads=%d must be a positive multiple of 16", num_heads);
+  if (topk <= 0 || topk % kMlaKeys != 0)
+    return set_error(kUnsupported, "sparse_mla: topk=%d must be a positive multiple of %d", topk, kMlaKeys);
+  if (kv_block_size <= 0 || kv_block_stride_bytes < (int64_t)kv_block_size * kMlaRowBytes)
+    return set_error(kInvalidArgument, "sparse_mla: kv block stride %lld < %d rows x 656 B",
+                     (long long)kv_block_stride_bytes, kv_block_size);
+  if (kv_block_stride_bytes % 16 != 0)
+    return set_error(kInvalidArgument, "sparse_mla: kv block stride must be a multiple of 16 bytes");
+  if (num_tokens == 0) return kOk;
+  if (!q || !kv_cache || !indices || !out)
+    return set_error(kInvalidArgument, "sparse_mla: null pointer");
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kv_cache) |
+       reinterpret_cast<uintptr_t>(out)) & 15)
+    return set_error(kInvalidArgument, "sparse_mla: q, kv_cache and out must be 16-byte aligned");
+  if ((q_token_stride % 8) || (q_head_stride % 8))
+    return set_error(kInvalidArgument, "sparse_mla: q strides must be multiples of 8 elements");
+  if (num_splits <= 0) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    num_splits = dsa_sparse_mla_num_splits(num_tokens, num_heads, topk, dsa_num_cus(dev));
+  }
+  if (num_splits > topk / kMlaKeys || (topk / num_splits) % kMlaKeys != 0 || topk % num_splits != 0)
+    return set_error(kInvalidArgument, "sparse_mla: num_splits=%d does not split topk=%d into 64-row blocks",
+                     num_splits, topk);
+  const size_t need = dsa_sparse_mla_workspace_bytes(num_tokens, num_heads, num_splits);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return set_error(kWorkspaceTooSmall, "sparse_mla: workspace %zu B < %zu B", workspace_bytes, need);
+
+  static int smem_status = -1;
+  if (smem_status < 0) {
+    smem_status = hipFuncSetAttribute((const void*)sparse_mla_kernel,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMlaSmemBytes) == hipSuccess
+                      ? 0 : 1;
+  }
+  if (smem_status) return set_error(kLaunchFailed, "sparse_mla: cannot reserve %zu B of LDS", kMlaSmemBytes);
+
+  MlaParams P;
+  P.q = static_cast<const uint16_t*>(q);
+  P.q_tok_stride = q_token_stride;
+  P.q_head_stride = q_head_stride;
+  P.kv = kv_cache;
+  P.kv_blk_stride = kv_block_stride_bytes;
+  P.kv_block_size = kv_block_size;
+  P.idx = indices;
+  P.idx_stride = idx_stride;
+  P.T = num_tokens;
+  P.H = num_heads;
+  P.topk = topk;
+  P.splits = num_splits;
+  P.head_groups = (num_heads + kMlaHeadsPerWG - 1) / kMlaHeadsPerWG;
+  P.scale_log2 = sm_scale * kLog2e;
+  P.out = static_cast<uint16_t*>(out);
+  P.lse = lse;
+  P.ws_o = nullptr;
+  P.ws_lse = nullptr;
+  if (num_splits > 1) {
+    const size_t rows = (size_t)num_splits * num_tokens * num_heads;
+    P.ws_o = static_cast<float*>(workspace);
+    P.ws_lse = P.ws_o + rows * kMlaDv;
+  }
+  const int64_t nwg = (int64_t)num_tokens * P.head_groups * num_splits;
+  hipLaunchKernelGGL(sparse_mla_kernel, dim3((unsigned)nwg), dim3(kMlaThreads), kMlaSmemBytes,
+                     (hipStream_t)stream, P);
+  if (int rc = check_launch("dsa_sparse_mla_decode")) return rc;
+  if (num_splits > 1) {
+    hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3((unsigned)(num_tokens * num_heads)), dim3(64), 0,
+                       (hipStream_t)stream, P.ws_o, P.ws_lse, num_tokens, num_heads, num_splits, P.out, lse);
+    return check_launch("dsa_sparse_mla_decode(combine)");
+  }
+  return kOk;
+}
+
+}  // extern "C"

@@ -1,0 +1,242 @@
+"""Tensor-level adapters over the C ABI (include/dsa_amd.h).
+
+Every function here validates shapes, dtypes, devices and strides the way the
+reference's ``TensorMatcher`` checks do (dlengine/runtime/kernel/jit/sgl/
+csrc/deepseek_v4/topk.cuh:350-378), then launches on the current HIP stream.
+Outputs are caller-allocated wherever the reference's are; nothing here
+synchronises the host, so the calls are capturable in a HIP graph.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+MLA_ROW_BYTES = 656
+MLA_D_QK = 576
+MLA_D_V = 512
+INDEXER_HEADS = 64
+INDEXER_HEAD_DIM = 128
+INDEXER_ROW_BYTES = INDEXER_HEAD_DIM + 4
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require(cond: bool, msg: str, exc=RuntimeError) -> None:
+    if not cond:
+        raise exc(msg)
+
+
+def _check_cuda(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        _require(t.is_cuda, f"tensor on {t.device}: the DSA path runs on the GPU only")
+        _require(t.device == dev, f"tensors on different devices: {t.device} vs {dev}")
+    return dev
+
+
+def _as_bytes(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.uint8 else t.view(torch.uint8)
+
+
+# --------------------------------------------------------------------------- device info
+def num_cus(device: int | torch.device | None = None) -> int:
+    if device is None:
+        device = torch.cuda.current_device()
+    if isinstance(device, torch.device):
+        device = device.index if device.index is not None else torch.cuda.current_device()
+    return int(_lib.load().dsa_num_cus(int(device)))
+
+
+def topk_max_len() -> int:
+    return int(_lib.load().dsa_topk_max_len())
+
+
+# --------------------------------------------------------------------------- indexer
+def indexer_schedule(context_lens: torch.Tensor, page_size: int) -> torch.Tensor:
+    cl = context_lens if context_lens.dim() == 2 else context_lens.reshape(-1, 1)
+    cl = cl.to(torch.int32).contiguous()
+    dev = _check_cuda(cl)
+    out = torch.empty(cl.shape[0] + 1, dtype=torch.int32, device=dev)
+    _lib.call("dsa_indexer_schedule", cl.data_ptr(), cl.shape[0], cl.shape[1], int(page_size),
+              out.data_ptr(), _stream(dev))
+    return out
+
+
+def indexer_logits(q_fp8: torch.Tensor, kv_cache: torch.Tensor, weights: torch.Tensor,
+                   context_lens: torch.Tensor, block_tables: torch.Tensor, max_context_len: int,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp8 paged indexer logits [B*n, max_context_len] f32 (see dsa_indexer_logits)."""
+    _require(q_fp8.dim() == 4, f"q_fp8 must be [B, next_n, H, D], got {tuple(q_fp8.shape)}")
+    B, n, H, D = q_fp8.shape
+    _require(q_fp8.dtype in (torch.float8_e4m3fn, torch.uint8), f"q_fp8 dtype {q_fp8.dtype}")
+    _require(q_fp8.is_contiguous(), "q_fp8 must be contiguous")
+    _require(kv_cache.dtype in (torch.uint8, torch.float8_e4m3fn), f"kv_cache dtype {kv_cache.dtype}")
+    _require(kv_cache.is_contiguous(), "kv_cache must be contiguous")
+    num_pages = kv_cache.shape[0]
+    _require(kv_cache.numel() % max(num_pages, 1) == 0, "kv_cache shape")
+    page_bytes = kv_cache.numel() // max(num_pages, 1)
+    _require(page_bytes % (D + 4) == 0, f"kv_cache page of {page_bytes} B is not page_size*{D + 4}")
+    page_size = page_bytes // (D + 4)
+    _require(weights.dtype == torch.float32 and tuple(weights.shape) == (B * n, H),
+             f"weights must be f32 [{B * n}, {H}], got {weights.dtype} {tuple(weights.shape)}")
+    weights = weights.contiguous()
+    cl = context_lens.reshape(B, -1)
+    _require(cl.shape[1] == n, f"context_lens must be [B, next_n]={B, n}, got {tuple(context_lens.shape)}")
+    cl = cl.to(torch.int32).contiguous()
+    _require(block_tables.dim() == 2 and block_tables.shape[0] == B, "block_tables must be [B, M]")
+    bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
+    _require(bt.stride(1) == 1, "block_tables rows must be contiguous")
+    _require(bt.shape[1] * page_size >= max_context_len, "block_tables too narrow for max_context_len")
+    dev = _check_cuda(q_fp8, kv_cache, weights, cl, bt)
+    if out is None:
+        out = torch.empty(B * n, max_context_len, dtype=torch.float32, device=dev)
+    _require(out.dtype == torch.float32 and out.shape[0] == B * n and out.shape[1] >= max_context_len
+             and out.stride(1) == 1, "logits output must be f32 [B*n, >=max_ctx] with unit column stride")
+    _lib.call("dsa_indexer_logits", _as_bytes(q_fp8).data_ptr(), _as_bytes(kv_cache).data_ptr(),
+              weights.data_ptr(), cl.data_ptr(), bt.data_ptr(), bt.stride(0), B, n, H, D, page_size,
+              int(max_context_len), out.data_ptr(), out.stride(0), _stream(dev))
+    return out
+
+
+# --------------------------------------------------------------------------- top-k
+def topk_transform(scores: torch.Tensor, seq_lens: torch.Tensor, page_tables: torch.Tensor,
+                   out_page_indices: torch.Tensor, page_size: int, top_k: int,
+                   out_raw_indices: torch.Tensor | None = None) -> None:
+    if top_k not in (512, 2048):
+        raise ValueError(f"top_k must be 512 or 2048, got {top_k}")
+    _require(scores.dim() == 2 and scores.dtype == torch.float32 and scores.stride(1) == 1,
+             "scores must be f32 [B, S] with unit column stride")
+    B = scores.shape[0]
+    _require(seq_lens.dtype == torch.int32 and tuple(seq_lens.shape) == (B,) and seq_lens.is_contiguous(),
+             "seq_lens must be contiguous int32 [B]")
+    _require(page_tables.dim() == 2 and page_tables.shape[0] == B and page_tables.dtype == torch.int32
+             and page_tables.stride(1) == 1, "page_tables must be int32 [B, P] with unit column stride")
+    for name, t in (("out_page_indices", out_page_indices), ("out_raw_indices", out_raw_indices)):
+        if t is not None:
+            _require(t.dtype == torch.int32 and tuple(t.shape) == (B, top_k) and t.is_contiguous(),
+                     f"{name} must be contiguous int32 [{B}, {top_k}]")
+    if page_size <= 0 or page_size & (page_size - 1):
+        raise RuntimeError("page_size must be power of 2")
+    dev = _check_cuda(scores, seq_lens, page_tables, out_page_indices)
+    _lib.call("dsa_topk_transform", scores.data_ptr(), scores.stride(0), seq_lens.data_ptr(),
+              page_tables.data_ptr(), page_tables.stride(0), out_page_indices.data_ptr(),
+              _ptr(out_raw_indices), B, scores.shape[1], int(page_size), int(top_k), _stream(dev))
+
+
+def topk_transform_raw(scores: torch.Tensor, seq_lens: torch.Tensor, out_indices: torch.Tensor,
+                       top_k: int) -> None:
+    """Exact top-k positions without translation (``page_table`` NULL in the C ABI)."""
+    if top_k not in (512, 2048):
+        raise ValueError(f"top_k must be 512 or 2048, got {top_k}")
+    _require(scores.dim() == 2 and scores.dtype == torch.float32 and scores.stride(1) == 1,
+             "scores must be f32 [B, S] with unit column stride")
+    B = scores.shape[0]
+    _require(seq_lens.dtype == torch.int32 and tuple(seq_lens.shape) == (B,) and seq_lens.is_contiguous(),
+             "seq_lens must be contiguous int32 [B]")
+    _require(out_indices.dtype == torch.int32 and tuple(out_indices.shape) == (B, top_k)
+             and out_indices.is_contiguous(), f"out_indices must be contiguous int32 [{B}, {top_k}]")
+    dev = _check_cuda(scores, seq_lens, out_indices)
+    _lib.call("dsa_topk_transform", scores.data_ptr(), scores.stride(0), seq_lens.data_ptr(), None, 0,
+              out_indices.data_ptr(), None, B, scores.shape[1], 1, int(top_k), _stream(dev))
+
+
+def topk_transform_ragged(scores: torch.Tensor, seq_lens: torch.Tensor, row_starts: torch.Tensor,
+                          offsets: torch.Tensor, out_indices: torch.Tensor, top_k: int) -> None:
+    if top_k != 2048:
+        raise ValueError(f"ragged Indexer top_k must be 2048, got {top_k}")
+    _require(scores.dim() == 2 and scores.dtype == torch.float32 and scores.stride(1) == 1,
+             "scores must be f32 [B, S] with unit column stride")
+    B = scores.shape[0]
+    for name, t in (("seq_lens", seq_lens), ("row_starts", row_starts), ("offsets", offsets)):
+        _require(t.dtype == torch.int32 and tuple(t.shape) == (B,) and t.is_contiguous(),
+                 f"{name} must be contiguous int32 [B]")
+    _require(out_indices.dtype == torch.int32 and tuple(out_indices.shape) == (B, top_k)
+             and out_indices.is_contiguous(), "out_indices must be contiguous int32 [B, top_k]")
+    dev = _check_cuda(scores, seq_lens, row_starts, offsets, out_indices)
+    _lib.call("dsa_topk_transform_ragged", scores.data_ptr(), scores.stride(0), seq_lens.data_ptr(),
+              row_starts.data_ptr(), offsets.data_ptr(), out_indices.data_ptr(), B, scores.shape[1],
+              int(top_k), _stream(dev))
+
+
+def topk_to_physical(topk_indices: torch.Tensor, block_table: torch.Tensor, block_size: int,
+                     rows_per_table: int = 1, out: torch.Tensor | None = None) -> torch.Tensor:
+    _require(topk_indices.dim() == 2 and topk_indices.dtype == torch.int32 and topk_indices.stride(1) == 1,
+             "topk_indices must be int32 [rows, topk] with unit column stride")
+    rows, k = topk_indices.shape
+    bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+    _require(bt.dim() == 2 and bt.stride(1) == 1, "block_table must be 2-D with unit column stride")
+    _require(rows == bt.shape[0] * rows_per_table,
+             f"rows {rows} != block_table rows {bt.shape[0]} x rows_per_table {rows_per_table}")
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    dev = _check_cuda(topk_indices, bt)
+    if out is None:
+        out = torch.empty(rows, k, dtype=torch.int32, device=dev)
+    _lib.call("dsa_topk_to_physical", topk_indices.data_ptr(), topk_indices.stride(0), bt.data_ptr(),
+              bt.stride(0), bt.shape[1], rows, k, int(rows_per_table), int(block_size), out.data_ptr(),
+              _stream(dev))
+    return out
+
+
+# --------------------------------------------------------------------------- sparse MLA
+def mla_kv_geometry(k_cache: torch.Tensor) -> tuple[int, int]:
+    """(block stride in bytes, rows per block) of an fp8 MLA cache view
+    [num_blocks, block_size, (1,) 656] whose block stride may include the
+    padding row (dlengine/runtime/context/cache/mla.py:164-182)."""
+    _require(k_cache.dtype in (torch.uint8, torch.float8_e4m3fn), f"k_cache dtype {k_cache.dtype}")
+    _require(k_cache.shape[-1] == MLA_ROW_BYTES and k_cache.stride(-1) == 1,
+             f"k_cache rows must be {MLA_ROW_BYTES} contiguous bytes")
+    _require(k_cache.dim() in (3, 4), "k_cache must be [blocks, block_size, (1,) 656]")
+    if k_cache.dim() == 4:
+        _require(k_cache.shape[2] == 1, "MLA cache has one KV head")
+    _require(k_cache.stride(1) == MLA_ROW_BYTES, "rows inside a block must be 656 B apart")
+    return k_cache.stride(0), k_cache.shape[1]
+
+
+def sparse_mla_workspace_bytes(num_tokens: int, num_heads: int, num_splits: int) -> int:
+    return int(_lib.load().dsa_sparse_mla_workspace_bytes(num_tokens, num_heads, num_splits))
+
+
+def sparse_mla_num_splits(num_tokens: int, num_heads: int, topk: int, device=None) -> int:
+    return int(_lib.load().dsa_sparse_mla_num_splits(num_tokens, num_heads, topk, num_cus(device)))
+
+
+def sparse_mla_decode(q: torch.Tensor, k_cache: torch.Tensor, indices: torch.Tensor, sm_scale: float,
+                      out: torch.Tensor | None = None, lse: torch.Tensor | None = None,
+                      num_splits: int | None = None,
+                      workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """q [T,H,576] bf16, indices [T,topk] int32 physical slots -> (o [T,H,512] bf16, lse [T,H] f32)."""
+    _require(q.dim() == 3 and q.shape[2] == MLA_D_QK and q.dtype == torch.bfloat16 and q.stride(2) == 1,
+             f"q must be bf16 [T, H, {MLA_D_QK}] with a contiguous last dim")
+    T, H, _ = q.shape
+    _require(indices.dim() == 2 and indices.shape[0] == T and indices.dtype == torch.int32
+             and indices.stride(1) == 1, "indices must be int32 [T, topk] with unit column stride")
+    topk = indices.shape[1]
+    blk_stride, block_size = mla_kv_geometry(k_cache)
+    dev = _check_cuda(q, k_cache, indices)
+    if out is None:
+        out = torch.empty(T, H, MLA_D_V, dtype=torch.bfloat16, device=dev)
+    if lse is None:
+        lse = torch.empty(T, H, dtype=torch.float32, device=dev)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H, MLA_D_V) and out.is_contiguous(),
+             "out must be contiguous bf16 [T, H, 512]")
+    _require(lse.dtype == torch.float32 and tuple(lse.shape) == (T, H) and lse.is_contiguous(),
+             "lse must be contiguous f32 [T, H]")
+    if num_splits is None:
+        num_splits = sparse_mla_num_splits(T, H, topk, dev)
+    need = sparse_mla_workspace_bytes(T, H, num_splits)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
+    ws_bytes = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
+    _lib.call("dsa_sparse_mla_decode", q.data_ptr(), q.stride(0), q.stride(1), _as_bytes(k_cache).data_ptr(),
+              blk_stride, block_size, indices.data_ptr(), indices.stride(0), T, H, topk, float(sm_scale),
+              out.data_ptr(), lse.data_ptr(), int(num_splits), ws_ptr, ws_bytes, _stream(dev))
+    return out, lse

@@ -1,0 +1,57 @@
+"""The full DSA decode step on one GPU: indexer logits -> exact top-k with page
+translation -> sparse MLA decode.
+
+This is the composition ``DeepseekV2Attention.forward`` performs per layer in
+decode (dlengine/runtime/models/deepseek_v2/deepseek_v2.py:1860-2018 calling
+``Indexer.forward`` lightning.py:1357-1466 with ``translate_topk=True`` and then
+``FlashMlaAttention.forward`` flash_mla.py:76-99). Every buffer is allocated
+once in the constructor, so a step is three kernel launches and no allocation
+(capturable in a HIP graph).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+class DsaDecodeStep:
+    def __init__(self, batch: int, next_n: int, max_context_len: int, num_heads: int = 128,
+                 index_topk: int = 2048, page_size: int = 64, device="cuda"):
+        self.batch, self.next_n, self.max_ctx = batch, next_n, max_context_len
+        self.num_heads, self.topk, self.page_size = num_heads, index_topk, page_size
+        rows = batch * next_n
+        dev = torch.device(device)
+        self.logits = torch.empty(rows, max_context_len, dtype=torch.float32, device=dev)
+        self.logical = torch.empty(rows, index_topk, dtype=torch.int32, device=dev)
+        self.physical = torch.empty(rows, index_topk, dtype=torch.int32, device=dev)
+        self.out = torch.empty(rows, num_heads, ops.MLA_D_V, dtype=torch.bfloat16, device=dev)
+        self.lse = torch.empty(rows, num_heads, dtype=torch.float32, device=dev)
+        self.num_splits = ops.sparse_mla_num_splits(rows, num_heads, index_topk, dev)
+        need = ops.sparse_mla_workspace_bytes(rows, num_heads, self.num_splits)
+        self.workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+
+    def expand_lens(self, context_lens: torch.Tensor) -> torch.Tensor:
+        """Per-query causal lengths, flattened [batch*next_n] int32."""
+        n = self.next_n
+        if n == 1:
+            return context_lens.to(torch.int32).reshape(-1).contiguous()
+        offs = torch.arange(n - 1, -1, -1, dtype=torch.int32, device=context_lens.device)
+        return (context_lens.to(torch.int32)[:, None] - offs).clamp_min(1).reshape(-1).contiguous()
+
+    def __call__(self, q_idx_fp8: torch.Tensor, weights: torch.Tensor, indexer_cache: torch.Tensor,
+                 seq_lens: torch.Tensor, block_tables: torch.Tensor, page_tables: torch.Tensor,
+                 q_mla: torch.Tensor, kv_cache: torch.Tensor, sm_scale: float):
+        """q_idx_fp8 [B*n, 64, 128] fp8; weights [B*n, 64] f32; indexer_cache
+        [pages, 8448] uint8; seq_lens [B*n] int32 per-query lengths;
+        block_tables [B, M] int32; page_tables [B*n, M] int32 (block_tables
+        repeated per query token); q_mla [B*n, H, 576] bf16; kv_cache
+        [blocks, 64, 1, 656] fp8 bytes. Returns (o, lse, logical, physical)."""
+        B, n = self.batch, self.next_n
+        ops.indexer_logits(q_idx_fp8.view(B, n, *q_idx_fp8.shape[1:]), indexer_cache, weights,
+                           seq_lens.view(B, n), block_tables, self.max_ctx, out=self.logits)
+        ops.topk_transform(self.logits, seq_lens, page_tables, self.physical, self.page_size, self.topk,
+                           self.logical)
+        ops.sparse_mla_decode(q_mla, kv_cache, self.physical, sm_scale, out=self.out, lse=self.lse,
+                              num_splits=self.num_splits, workspace=self.workspace)
+        return self.out, self.lse, self.logical, self.physical

@@ -1,0 +1,398 @@
+"""CPU restatement of the reference DSA decode path, in numpy.
+
+TEST INFRASTRUCTURE ONLY. Imported by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` as the checker; nothing in
+``nanoengine_amd`` imports it, and it is never what is measured or shipped.
+
+Every function cites the reference file:line it follows (paths relative to the
+reference repository root, package ``dlengine``). Numerics:
+
+* fp8 is OCP ``float8_e4m3fn`` (bias 7, no infinities, 0x7f/0xff = NaN,
+  max finite 448), stored as raw ``uint8`` bytes.
+* bf16 is stored as raw ``uint16`` (the upper half of an IEEE f32).
+* Accumulation is float64 unless stated, so the oracle sits closer to the exact
+  value than any fp32 kernel; tolerances in the tests absorb the kernels'
+  fp32 accumulation order.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "FP8_MAX", "D_NOPE", "D_ROPE", "D_QK", "MLA_ROW_BYTES", "MLA_TILE",
+    "fp8_e4m3fn_decode", "fp8_e4m3fn_encode", "bf16_to_f32", "f32_to_bf16",
+    "ue8m0_ceil", "quantize_rows_ue8m0", "pack_indexer_cache", "indexer_cache_token",
+    "quantize_mla_rows", "unpack_mla_rows", "dequant_mla_rows",
+    "expand_decode_context_lens", "indexer_logits", "indexer_logits_bruteforce",
+    "topk_select", "topk_transform", "topk_transform_ragged",
+    "topk_indices_to_physical", "sparse_mla_decode", "indexer_decode_topk",
+]
+
+FP8_MAX = 448.0
+D_NOPE = 512          # fp8_utils.py:13
+D_ROPE = 64           # fp8_utils.py:14
+D_QK = D_NOPE + D_ROPE
+MLA_TILE = 128        # fp8_utils.py:16
+MLA_ROW_BYTES = D_NOPE + (D_NOPE // MLA_TILE) * 4 + D_ROPE * 2   # 656, fp8_utils.py:21
+INDEXER_HEAD_DIM = 128
+INDEXER_ROW_BYTES = INDEXER_HEAD_DIM + 4                            # 132, lightning.py:411-413
+
+
+# --------------------------------------------------------------------------- fp8 / bf16
+def _build_e4m3fn_table() -> np.ndarray:
+    """Decode table for all 256 e4m3fn codes, from the OCP bit layout."""
+    tab = np.empty(256, dtype=np.float64)
+    for code in range(256):
+        s = -1.0 if code & 0x80 else 1.0
+        e = (code >> 3) & 0xF
+        m = code & 0x7
+        if e == 0xF and m == 0x7:
+            tab[code] = np.nan
+        elif e == 0:
+            tab[code] = s * m * 2.0 ** -9          # subnormal: m/8 * 2^(1-7)
+        else:
+            tab[code] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return tab
+
+
+_E4M3_TABLE = _build_e4m3fn_table()
+_E4M3_POS = _E4M3_TABLE[:127]                        # codes 0..126: 0 .. 448, increasing
+
+
+def fp8_e4m3fn_decode(codes: np.ndarray) -> np.ndarray:
+    """uint8 e4m3fn codes -> float32 values."""
+    return _E4M3_TABLE[np.asarray(codes, dtype=np.uint8)].astype(np.float32)
+
+
+def fp8_e4m3fn_encode(x: np.ndarray) -> np.ndarray:
+    """float -> e4m3fn codes, round-to-nearest-even, NaN for |x| beyond the
+    rounding range of 448 (the non-saturating cast ``tensor.to(float8_e4m3fn)``
+    used at lightning.py:92-97 and fp8_utils.py:55)."""
+    x = np.asarray(x, dtype=np.float64)
+    a = np.abs(x)
+    # nearest representable magnitude among the 127 finite non-negative codes
+    hi = np.searchsorted(_E4M3_POS, a, side="left").clip(0, 126)
+    lo = (hi - 1).clip(0, 126)
+    dhi = np.abs(_E4M3_POS[hi] - a)
+    dlo = np.abs(a - _E4M3_POS[lo])
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo).astype(np.uint8)
+    # the next step above 448 would be 480 (the NaN code): [448, 464] rounds
+    # to 448 (464 is the tie, even code wins), beyond that is NaN
+    over = a > 464.0
+    code = np.where(over | np.isnan(a), 0x7F, code).astype(np.uint8)
+    neg = (np.signbit(x)) & ~np.isnan(a)
+    return (code | np.where(neg, 0x80, 0).astype(np.uint8)).astype(np.uint8)
+
+
+def bf16_to_f32(u16: np.ndarray) -> np.ndarray:
+    return (np.asarray(u16, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round-to-nearest-even (NaN kept quiet)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    return np.where(nan, 0x7FC0, rounded).astype(np.uint16)
+
+
+def ue8m0_ceil(scale: np.ndarray) -> np.ndarray:
+    """Round a positive scale up to a power of two (UE8M0): lightning.py:91-92,
+    fp8_utils.py:27-29 ``2^ceil(log2(s))``."""
+    s = np.asarray(scale, dtype=np.float32)
+    return np.exp2(np.ceil(np.log2(s))).astype(np.float32)
+
+
+# --------------------------------------------------------------------------- indexer formats
+def quantize_rows_ue8m0(x: np.ndarray, min_amax: float = 1e-4):
+    """Per-row (128-wide) fp8 quantisation with a UE8M0 scale.
+
+    Follows ``_per_token_cast_to_fp8_ue8m0`` lightning.py:78-101 and the
+    ``quant_fp8(..., round_ue8m0=True, min_absmax=1e-4)`` call at
+    lightning.py:1327-1332: ``sf = 2^ceil(log2(max(amax,1e-4)/448))``,
+    ``code = e4m3fn(x / sf)``. ``x`` is [..., 128] float32 (bf16 values).
+    Returns (codes uint8 [...,128], scale float32 [...]).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    amax = np.abs(x).max(axis=-1)
+    amax = np.maximum(amax, np.float32(min_amax))
+    sf = ue8m0_ceil(amax / np.float32(FP8_MAX))
+    # multiply by the reciprocal as lightning.py:95 does (exact: sf is 2^k)
+    codes = fp8_e4m3fn_encode(x * (np.float32(1.0) / sf)[..., None])
+    return codes, sf
+
+
+def pack_indexer_cache(codes: np.ndarray, scales: np.ndarray, slots: np.ndarray,
+                       num_pages: int, page_size: int = 64) -> np.ndarray:
+    """Scatter per-token (fp8[128], f32 scale) into the split page layout
+    ``[page_size*128 fp8][page_size*4 scale]`` (lightning.py:494-507,
+    IndexerCache docstring :410-413). Returns uint8 [num_pages, page_size*132]."""
+    buf = np.zeros((num_pages, page_size * INDEXER_ROW_BYTES), dtype=np.uint8)
+    sc_bytes = np.asarray(scales, dtype=np.float32).reshape(-1, 1).view(np.uint8)
+    for tok, slot in enumerate(np.asarray(slots).tolist()):
+        page, off = divmod(int(slot), page_size)
+        buf[page, off * 128:(off + 1) * 128] = codes[tok]
+        base = page_size * 128 + off * 4
+        buf[page, base:base + 4] = sc_bytes[tok]
+    return buf
+
+
+def indexer_cache_token(cache: np.ndarray, slot: int, page_size: int = 64):
+    """Read one token back out of the split page layout -> (codes[128], scale)."""
+    page, off = divmod(int(slot), page_size)
+    codes = cache[page, off * 128:(off + 1) * 128]
+    base = page_size * 128 + off * 4
+    scale = cache[page, base:base + 4].copy().view(np.float32)[0]
+    return codes, scale
+
+
+# --------------------------------------------------------------------------- MLA row format
+def quantize_mla_rows(kv: np.ndarray) -> np.ndarray:
+    """[N,576] bf16-valued float32 -> [N,656] uint8 packed rows.
+
+    ``quantize_nope_fp8`` fp8_utils.py:32-58 (per-128-tile
+    ``scale = 2^ceil(log2(max(amax/448, 1e-12)))``, ``code = e4m3fn(v/scale)``)
+    then ``pack_mla_fp8`` fp8_utils.py:80-108 (bytes [0,512) fp8, [512,528)
+    4 x f32 scales, [528,656) 64 x bf16 rope).
+    """
+    kv = np.asarray(kv, dtype=np.float32)
+    n = kv.shape[0]
+    nope = kv[:, :D_NOPE].reshape(n, D_NOPE // MLA_TILE, MLA_TILE)
+    amax = np.abs(nope).max(axis=-1)
+    scales = np.exp2(np.ceil(np.log2(np.maximum(amax / np.float32(FP8_MAX),
+                                                np.float32(1e-12))))).astype(np.float32)
+    codes = fp8_e4m3fn_encode(nope / scales[..., None]).reshape(n, D_NOPE)
+    out = np.empty((n, MLA_ROW_BYTES), dtype=np.uint8)
+    out[:, :D_NOPE] = codes
+    out[:, D_NOPE:D_NOPE + 16] = scales.view(np.uint8).reshape(n, 16)
+    out[:, D_NOPE + 16:] = f32_to_bf16(kv[:, D_NOPE:]).view(np.uint8).reshape(n, 128)
+    return out
+
+
+def unpack_mla_rows(rows: np.ndarray):
+    """``unpack_mla_fp8`` fp8_utils.py:111-134 -> (codes [N,512], scales [N,4], rope bf16 bits [N,64])."""
+    rows = np.ascontiguousarray(rows, dtype=np.uint8)
+    codes = rows[:, :D_NOPE]
+    scales = rows[:, D_NOPE:D_NOPE + 16].copy().view(np.float32)
+    rope = rows[:, D_NOPE + 16:].copy().view(np.uint16)
+    return codes, scales, rope
+
+
+def dequant_mla_rows(rows: np.ndarray) -> np.ndarray:
+    """``dequantize_and_unpack_mla`` fp8_utils.py:153-177 -> [N,576] float32.
+    fp8 * power-of-two scale is exact in bf16, so the reference's bf16 cast
+    (fp8_utils.py:76) changes nothing for finite in-range values."""
+    codes, scales, rope = unpack_mla_rows(rows)
+    n = codes.shape[0]
+    nope = fp8_e4m3fn_decode(codes).reshape(n, 4, MLA_TILE) * scales[..., None]
+    out = np.empty((n, D_QK), dtype=np.float32)
+    out[:, :D_NOPE] = bf16_to_f32(f32_to_bf16(nope.reshape(n, D_NOPE)))
+    out[:, D_NOPE:] = bf16_to_f32(rope)
+    return out
+
+
+# --------------------------------------------------------------------------- indexer
+def expand_decode_context_lens(context_lens: np.ndarray, next_n: int) -> np.ndarray:
+    """``_expand_decode_context_lens`` lightning.py:350-378: per-query causal
+    length ``ctx - (next_n-1-j)`` clamped to >= 1, shape [B, next_n] int32."""
+    c = np.asarray(context_lens)
+    if c.ndim == 1:
+        c = c[:, None]
+    if c.ndim != 2 or c.shape[1] not in (1, next_n):
+        raise ValueError(
+            "Indexer context_lens must have shape [batch], [batch, 1], or "
+            f"[batch, next_n]; got {tuple(c.shape)} for next_n={next_n}")
+    if c.shape[1] == next_n:
+        return c.astype(np.int32)
+    offs = np.arange(next_n - 1, -1, -1, dtype=np.int64)
+    return np.maximum(c.astype(np.int64) - offs[None, :], 1).astype(np.int32)
+
+
+def indexer_logits(q_fp8: np.ndarray, kv_cache: np.ndarray, weights: np.ndarray,
+                   context_lens: np.ndarray, block_tables: np.ndarray,
+                   max_context_len: int, page_size: int = 64) -> np.ndarray:
+    """Paged fp8 lightning-indexer logits (the contract of
+    ``deep_gemm.fp8_paged_mqa_logits`` as called at lightning.py:1395-1406).
+
+    ``logits[b*n+j, t] = sum_h w[b*n+j,h] * relu(q[b,j,h,:] . k[t,:]) * s_k[t]``
+    (lightning.py:116-131 ``_weighted_relu_mqa_scores``; tilelang
+    fp8_index.py:81-92; ``w`` already folds q_scale, lightning.py:1252-1273).
+    q_fp8 uint8 [B,n,H,128]; kv_cache uint8 [pages, page_size*132];
+    weights f32 [B*n,H]; context_lens int [B,n]; block_tables int [B,M].
+    Positions t >= context_lens[b,j] are set to -inf (the reference leaves them
+    unspecified; the top-k never selects them).
+    """
+    B, n, H, D = q_fp8.shape
+    cl = expand_decode_context_lens(context_lens, n)
+    out = np.full((B * n, max_context_len), -np.inf, dtype=np.float32)
+    qf = fp8_e4m3fn_decode(q_fp8).astype(np.float64)
+    w = np.asarray(weights, dtype=np.float64).reshape(B, n, H)
+    for b in range(B):
+        L = int(cl[b].max())
+        if L <= 0:
+            continue
+        npages = (L + page_size - 1) // page_size
+        pages = np.asarray(block_tables[b, :npages], dtype=np.int64)
+        blk = kv_cache[pages]                                   # [np, P*132]
+        k = fp8_e4m3fn_decode(blk[:, :page_size * D].reshape(-1, D)).astype(np.float64)
+        s = blk[:, page_size * D:].copy().view(np.float32).reshape(-1).astype(np.float64)
+        k, s = k[:L], s[:L]
+        for j in range(n):
+            dots = np.einsum("hd,td->ht", qf[b, j], k)          # [H, L]
+            lg = (np.maximum(dots, 0.0) * w[b, j][:, None]).sum(axis=0) * s
+            Lj = int(cl[b, j])
+            out[b * n + j, :Lj] = lg[:Lj].astype(np.float32)
+    return out
+
+
+def indexer_logits_bruteforce(q: np.ndarray, w: np.ndarray, k: np.ndarray,
+                              s: np.ndarray) -> np.ndarray:
+    """Scalar-loop form of the weighted-ReLU score for tiny inputs (an
+    independent check of :func:`indexer_logits`): q [H,D], w [H], k [T,D], s [T]."""
+    H, D = q.shape
+    T = k.shape[0]
+    out = []
+    for t in range(T):
+        acc = 0.0
+        for h in range(H):
+            dot = 0.0
+            for d in range(D):
+                dot += float(q[h, d]) * float(k[t, d])
+            acc += float(w[h]) * max(dot, 0.0)
+        out.append(acc * float(s[t]))
+    return np.asarray(out, dtype=np.float64)
+
+
+# --------------------------------------------------------------------------- top-k
+def _order_keys(x: np.ndarray) -> np.ndarray:
+    """Monotone uint32 key of float32 (NaN mapped to -inf first)."""
+    x = np.where(np.isnan(x), -np.inf, x).astype(np.float32)
+    u = x.view(np.uint32)
+    return np.where(u & 0x80000000, ~u, u | 0x80000000).astype(np.uint32)
+
+
+def topk_select(row: np.ndarray, length: int, k: int) -> np.ndarray:
+    """Exact top-k positions of ``row[:length]``.
+
+    Set semantics follow ``torch.topk`` on the valid prefix
+    (lightning.py:1480-1482; topk.cuh:249-287 treats positions >= seq_len as
+    absent). The reference leaves the order of equal values unspecified; this
+    restatement fixes it: among equal scores the lowest positions win, and NaN
+    ranks as -inf. Returns the selected positions sorted ascending; when
+    ``length <= k`` that is ``0..length-1`` (topk.cuh:58-81).
+    """
+    length = int(length)
+    if length <= k:
+        return np.arange(max(length, 0), dtype=np.int32)
+    keys = _order_keys(np.asarray(row[:length], dtype=np.float32)).astype(np.int64)
+    order = np.lexsort((np.arange(length), -keys))            # key desc, index asc
+    return np.sort(order[:k]).astype(np.int32)
+
+
+def topk_transform(scores: np.ndarray, seq_lens: np.ndarray, page_tables: np.ndarray,
+                   page_size: int, top_k: int):
+    """``topk_transform`` deepseek_v4.py:324-367 -> kernel topk.cuh:249-287.
+
+    Per row: select the top ``top_k`` positions among ``[0, seq_len)``, write
+    them as logical positions (``raw``) and as physical slots
+    ``(page_table[p >> bits] << bits) | (p & mask)`` (topk.cuh:52-56); pad with
+    -1. Returns (page_indices, raw_indices), both int32 [B, top_k]; positions
+    are in ascending order.
+    """
+    if top_k not in (512, 2048):
+        raise ValueError(f"top_k must be 512 or 2048, got {top_k}")
+    if page_size <= 0 or page_size & (page_size - 1):
+        raise ValueError("page_size must be power of 2")
+    bits = page_size.bit_length() - 1
+    B = scores.shape[0]
+    page = np.full((B, top_k), -1, dtype=np.int32)
+    raw = np.full((B, top_k), -1, dtype=np.int32)
+    for b in range(B):
+        sel = topk_select(scores[b], int(seq_lens[b]), top_k)
+        raw[b, :sel.size] = sel
+        pt = np.asarray(page_tables[b], dtype=np.int64)
+        page[b, :sel.size] = ((pt[sel >> bits] << bits) | (sel & (page_size - 1))).astype(np.int32)
+    return page, raw
+
+
+def topk_transform_ragged(scores: np.ndarray, seq_lens: np.ndarray, row_starts: np.ndarray,
+                          offsets: np.ndarray, top_k: int) -> np.ndarray:
+    """``topk_transform_ragged`` deepseek_v4.py:370-388 -> topk.cuh:289-316:
+    top-k over ``scores[b, row_start : row_start+len]`` plus ``offsets[b]``;
+    ``len <= top_k`` emits ``i + offset`` for i < len, then -1. Exact here (the
+    reference's bounded candidate buffer may differ by <= 5 entries)."""
+    if top_k != 2048:
+        raise ValueError(f"ragged Indexer top_k must be 2048, got {top_k}")
+    B = scores.shape[0]
+    out = np.full((B, top_k), -1, dtype=np.int32)
+    for b in range(B):
+        L, r0, off = int(seq_lens[b]), int(row_starts[b]), int(offsets[b])
+        sel = topk_select(scores[b, r0:r0 + max(L, 0)], L, top_k)
+        out[b, :sel.size] = sel + off
+    return out
+
+
+def topk_indices_to_physical(topk_indices: np.ndarray, block_table: np.ndarray,
+                             block_size: int) -> np.ndarray:
+    """``topk_indices_to_physical`` mla_utils.py:237-272:
+    ``block_table[b, idx // bs] * bs + idx % bs``, -1 preserved."""
+    t = np.asarray(topk_indices, dtype=np.int64)
+    valid = t >= 0
+    safe = np.where(valid, t, 0)
+    blk = np.take_along_axis(np.asarray(block_table, dtype=np.int64), safe // block_size, axis=1)
+    phys = blk * block_size + safe % block_size
+    return np.where(valid, phys, -1).astype(np.int32)
+
+
+def indexer_decode_topk(logits: np.ndarray, context_lens: np.ndarray, index_topk: int) -> np.ndarray:
+    """The portable selection tail of ``Indexer.forward`` lightning.py:1468-1492:
+    mask ``t >= ctx`` and non-finite/|x|>=1e30 to -inf, top-k, indices >= ctx
+    -> -1, pad to ``index_topk`` with -1. Returns logical positions
+    (ascending, ties to the lowest position) int32 [rows, index_topk]."""
+    rows, max_ctx = logits.shape
+    ctx = np.asarray(context_lens).reshape(-1)
+    out = np.full((rows, index_topk), -1, dtype=np.int32)
+    for r in range(rows):
+        L = int(ctx[r])
+        x = np.asarray(logits[r, :max_ctx], dtype=np.float32).copy()
+        bad = ~np.isfinite(x) | (np.abs(x) >= 1e30)
+        x[bad] = -np.inf
+        sel = topk_select(x, min(L, max_ctx), index_topk)
+        out[r, :sel.size] = sel
+    return out
+
+
+# --------------------------------------------------------------------------- sparse MLA
+def sparse_mla_decode(q: np.ndarray, kv_rows: np.ndarray, indices: np.ndarray,
+                      sm_scale: float, d_v: int = D_NOPE):
+    """Absorbed sparse MLA decode over packed fp8 rows (the contract of
+    ``flash_mla.flash_mla_with_kvcache(..., is_fp8_kvcache=True, indices=...)``
+    flash_mla.py:76-99).
+
+    q float32 [T,H,576] (bf16 values); kv_rows uint8 [num_slots,656] addressed
+    by physical slot; indices int [T,K], -1 = skip (mla_utils.py:267-271).
+    Per (t,h): ``s_i = scale * q . kv(idx_i)`` over valid i, ``o = softmax(s) @
+    kv(idx)[:, :512]`` (test_mla_decode_head_padding.py:30-33), and the natural
+    log LSE ``log sum_i exp(s_i)`` (the convention of
+    ``merge_attention_states`` mla_utils.py:19-21). Rows dequantise as
+    fp8_utils.py:153-177. A query with no valid index gives o = 0, lse = -inf.
+    Returns (o float32 [T,H,d_v], lse float32 [T,H]).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    T, H, D = q.shape
+    o = np.zeros((T, H, d_v), dtype=np.float32)
+    lse = np.full((T, H), -np.inf, dtype=np.float32)
+    for t in range(T):
+        idx = np.asarray(indices[t]).astype(np.int64)
+        idx = idx[idx >= 0]
+        if idx.size == 0:
+            continue
+        kv = dequant_mla_rows(kv_rows[idx]).astype(np.float64)   # [n, 576]
+        s = (q[t] @ kv[:, :D].T) * sm_scale                      # [H, n]
+        m = s.max(axis=1, keepdims=True)
+        p = np.exp(s - m)
+        den = p.sum(axis=1, keepdims=True)
+        o[t] = ((p / den) @ kv[:, :d_v]).astype(np.float32)
+        lse[t] = (m[:, 0] + np.log(den[:, 0])).astype(np.float32)
+    return o, lse

@@ -1,0 +1,116 @@
+"""Sparse MLA decode on the GPU vs the CPU oracle.
+
+Tolerances (north star): o within bf16 atol 2e-2, LSE within 1e-3 (absolute,
+natural log). The rows' fp8 values dequantise exactly into bf16, so the only
+differences are bf16 rounding of P and fp32 accumulation order.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from nanoengine_amd import flash_mla, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(T, H, K, num_blocks, seed, invalid_frac=0.0, device="cuda"):
+    kv = synth.make_mla_cache(num_blocks, seed=seed, device=device)
+    q = synth.make_mla_query(T, H, seed=seed, device=device)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    idx = torch.stack([torch.randperm(num_blocks * 64, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    if invalid_frac:
+        idx[torch.rand(T, K, generator=g) < invalid_frac] = -1
+    return q, kv, idx.to(device)
+
+
+def _oracle(q, kv, idx, scale):
+    rows = kv.reshape(-1, 656).cpu().numpy() if kv.is_contiguous() else \
+        kv.contiguous().reshape(-1, 656).cpu().numpy()
+    qf = q.float().cpu().numpy()
+    return O.sparse_mla_decode(qf, rows, idx.cpu().numpy(), scale)
+
+
+def _check(o, lse, eo, elv):
+    o = o.float().cpu().numpy()
+    lse = lse.cpu().numpy()
+    assert np.abs(o - eo).max() <= 2e-2
+    fin = np.isfinite(elv)
+    assert np.array_equal(np.isfinite(lse), fin)
+    assert np.abs(lse[fin] - elv[fin]).max() <= 1e-3
+
+
+@pytest.mark.parametrize("T,H,K,splits", [(2, 128, 2048, 1), (3, 128, 512, 4), (4, 64, 256, 2), (2, 16, 128, 1)])
+def test_matches_oracle(cuda, T, H, K, splits):
+    q, kv, idx = _case(T, H, K, num_blocks=80, seed=T * 1000 + K)
+    scale = 192 ** -0.5
+    # oracle addresses slots as block*64+row in a dense [blocks*64, 656] view
+    o, lse = ops.sparse_mla_decode(q, kv, idx, scale, num_splits=splits)
+    torch.cuda.synchronize()
+    eo, elv = _oracle(q, kv, idx, scale)
+    _check(o, lse, eo, elv)
+
+
+def test_invalid_indices_and_empty_rows(cuda):
+    q, kv, idx = _case(3, 128, 1024, num_blocks=40, seed=3, invalid_frac=0.3)
+    idx[1] = -1                         # a query with no valid index: o = 0, lse = -inf
+    idx[2, 64:] = -1                    # only the first block valid
+    scale = 192 ** -0.5
+    for splits in (1, 4):
+        o, lse = ops.sparse_mla_decode(q, kv, idx, scale, num_splits=splits)
+        torch.cuda.synchronize()
+        eo, elv = _oracle(q, kv, idx, scale)
+        _check(o, lse, eo, elv)
+        assert torch.all(o[1] == 0) and torch.all(torch.isneginf(lse[1]))
+
+
+def test_split_counts_agree(cuda):
+    q, kv, idx = _case(2, 128, 2048, num_blocks=64, seed=8)
+    outs = [ops.sparse_mla_decode(q, kv, idx, 0.07, num_splits=s) for s in (1, 2, 8, 32)]
+    torch.cuda.synchronize()
+    base_o, base_l = outs[0]
+    for o, l in outs[1:]:
+        assert (o.float() - base_o.float()).abs().max().item() <= 1e-2
+        assert (l - base_l).abs().max().item() <= 1e-4
+
+
+def test_flash_mla_signature_and_dense_reference(cuda):
+    # the reference's dense einsum check (tests/test_mla_decode_head_padding.py:30-33)
+    B, n, H, K = 2, 2, 128, 512
+    q, kv, idx = _case(B * n, H, K, num_blocks=32, seed=21)
+    sched, _ = flash_mla.get_mla_metadata()
+    o, lse = flash_mla.flash_mla_with_kvcache(q.view(B, n, H, 576), kv, None, None, 512, sched, None,
+                                              192 ** -0.5, False, is_fp8_kvcache=True,
+                                              indices=idx.view(B, n, K))
+    torch.cuda.synchronize()
+    assert o.shape == (B, n, H, 512) and lse.shape == (B, H, n)
+    rows = torch.from_numpy(O.dequant_mla_rows(kv.contiguous().reshape(-1, 656).cpu().numpy()))
+    sel = rows[idx.cpu().long()]                                     # [T, K, 576]
+    scores = torch.einsum("thd,tkd->thk", q.float().cpu(), sel) * 192 ** -0.5
+    ref = torch.einsum("thk,tkv->thv", scores.softmax(-1), sel[..., :512])
+    diff = o.reshape(B * n, H, 512).float().cpu() - ref
+    assert diff.norm() / ref.norm() < 0.006
+    torch.testing.assert_close(lse.permute(0, 2, 1).reshape(B * n, H).cpu(), torch.logsumexp(scores, -1),
+                               atol=1e-3, rtol=0)
+
+
+def test_graph_capture_replays_match_eager(cuda):
+    q, kv, idx = _case(4, 128, 2048, num_blocks=64, seed=5)
+    out = torch.empty(4, 128, 512, dtype=torch.bfloat16, device=cuda)
+    lse = torch.empty(4, 128, dtype=torch.float32, device=cuda)
+    splits = 4
+    ws = torch.empty(ops.sparse_mla_workspace_bytes(4, 128, splits), dtype=torch.uint8, device=cuda)
+    ops.sparse_mla_decode(q, kv, idx, 0.1, out=out, lse=lse, num_splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    eager_o, eager_l = out.clone(), lse.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ops.sparse_mla_decode(q, kv, idx, 0.1, out=out, lse=lse, num_splits=splits, workspace=ws)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_o) and torch.equal(lse, eager_l)
