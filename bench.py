@@ -1,0 +1,224 @@
+"""DSA decode step benchmark on one MI355X.
+
+One step = indexer logits (fp8 MFMA over the paged indexer cache) -> exact
+top-2048 with page translation -> sparse MLA decode over the paged fp8 MLA
+cache, for batch 128, next_n 1, 64K context per sequence, 64 indexer heads x
+128, 128 MLA heads x 576/512. Inputs are seeded synthetic data already resident
+in HBM; block tables are a random permutation of the page pool.
+
+Prints ONE JSON line. `value` is decode tokens/s (= batch / step time);
+`roofline` covers the dominant kernel (the indexer, HBM-bound), measured with
+HIP events on the stream the kernels run on; `stages` reports every kernel;
+`cpu_baseline` times the numpy oracle of the same step on a bounded sample of
+the sequences on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       python bench.py --copy-calib   (a plain 1 GiB device copy, for scaling
+                                       rocprofv3 FETCH_SIZE/WRITE_SIZE)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "DSA decode µs/step & tokens/s at B=128,64K ctx,k=2048; % HBM / fp8-MFMA peak"
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "indexer_config2_pmc.txt")
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--batch", type=int, default=128)
+    p.add_argument("--ctx", type=int, default=65536)
+    p.add_argument("--heads", type=int, default=128)
+    p.add_argument("--topk", type=int, default=2048)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample")
+    p.add_argument("--copy-calib", action="store_true")
+    return p.parse_args()
+
+
+def pmc_traffic():
+    """HBM bytes per indexer launch from the committed rocprofv3 PMC summary, if any."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read(), re.M)
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def copy_calib():
+    import torch
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "launches": 5}))
+
+
+def cpu_baseline(inp, kv, q_mla, lens, sample, scale, topk):
+    """Times the numpy oracle of the full step for `sample` sequences."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    import oracle as O
+
+    cores = min(os.cpu_count() or 1, 16)
+    bt_all = inp.block_tables[:sample].cpu().numpy()
+    used = np.unique(bt_all.reshape(-1))
+    # the sample's pages, renumbered densely (same bytes, smaller arrays)
+    remap = np.full(int(bt_all.max()) + 1, -1, np.int64)
+    remap[used] = np.arange(used.size)
+    bt = remap[bt_all].astype(np.int32)
+    idx_cache = inp.cache[torch.from_numpy(used).to(inp.cache.device)].cpu().numpy()
+    kv_rows = kv[torch.from_numpy(used).to(kv.device)].contiguous().reshape(-1, 656).cpu().numpy()
+    q_idx = inp.q_fp8[:sample].cpu().numpy().reshape(sample, 1, 64, 128)
+    w = inp.weights[:sample].cpu().numpy()
+    qm = q_mla[:sample].float().cpu().numpy()
+    ctx = np.asarray(lens[:sample], dtype=np.int32).reshape(sample, 1)
+    max_ctx = bt.shape[1] * 64
+    with threadpool_limits(limits=cores):
+        t0 = time.perf_counter()
+        logits = O.indexer_logits(q_idx, idx_cache, w, ctx, bt, max_ctx)
+        page, raw = O.topk_transform(logits, ctx.reshape(-1), bt, 64, topk)
+        O.sparse_mla_decode(qm, kv_rows, page, scale)
+        dt = time.perf_counter() - t0
+    return {"value": sample / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{sample} of {len(lens)} sequences of the same workload (numpy oracle: indexer "
+                      f"logits + exact top-{topk} + transform + sparse MLA), {dt:.1f} s"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the DSA decode path is "
+              "rank-local and this build measures one GPU's share", file=sys.stderr)
+        sys.exit(2)
+    if args.copy_calib:
+        copy_calib()
+        return
+
+    import torch
+
+    from nanoengine_amd import _lib, synth
+    from nanoengine_amd.pipeline import DsaDecodeStep
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    B, L, H, K = args.batch, args.ctx, args.heads, args.topk
+    lens = [L] * B
+    inp = synth.make_indexer_inputs(lens, next_n=1, seed=args.seed, device=dev)
+    num_blocks = int(inp.block_tables.max().item()) + 1
+    kv = synth.make_mla_cache(num_blocks, seed=args.seed, device=dev)
+    q_mla = synth.make_mla_query(B, H, seed=args.seed, device=dev)
+    scale = 192 ** -0.5
+    max_ctx = inp.block_tables.shape[1] * 64
+    step = DsaDecodeStep(B, 1, max_ctx, num_heads=H, index_topk=K, device=dev)
+    seq = inp.context_lens
+    bt = inp.block_tables
+    torch.cuda.synchronize()
+
+    def run(ev=None):
+        from nanoengine_amd import ops
+        if ev is not None:
+            ev[0].record()
+        ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+                           max_ctx, out=step.logits)
+        if ev is not None:
+            ev[1].record()
+        ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical)
+        if ev is not None:
+            ev[2].record()
+        ops.sparse_mla_decode(q_mla, kv, step.physical, scale, out=step.out, lse=step.lse,
+                              num_splits=step.num_splits, workspace=step.workspace)
+        if ev is not None:
+            ev[3].record()
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` steps, synchronised on both sides
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    # per-stage durations with HIP events on the launch stream (separate pass)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for e in evs:
+        run(e)
+    torch.cuda.synchronize()
+    st = [[e[i].elapsed_time(e[i + 1]) * 1e3 for e in evs] for i in range(3)]   # us
+    med = [sorted(x)[len(x) // 2] for x in st]
+    avg = [sum(x) / len(x) for x in st]
+
+    total_tokens = sum(lens)
+    idx_bytes = total_tokens * 132 + B * 64 * 128 + B * 64 * 4 + B * max_ctx * 4
+    idx_flops = 2.0 * 64 * 128 * total_tokens
+    topk_bytes = B * max_ctx * 4 * 2 + B * K * 4 * 2 + B * (max_ctx // 64) * 4
+    valid = int((step.physical >= 0).sum().item())
+    mla_bytes = valid * 656 + B * H * 576 * 2 + B * H * 512 * 2 + B * H * 4 + B * K * 4
+    mla_flops = 2.0 * H * (576 + 512) * valid
+
+    def gbs(b, us):
+        return b / (us * 1e-6) / 1e9
+
+    stages = {
+        "indexer_logits": {"us": round(avg[0], 2), "us_median": round(med[0], 2), "bytes": idx_bytes,
+                           "GBps": round(gbs(idx_bytes, avg[0]), 1),
+                           "hbm_frac": round(gbs(idx_bytes, avg[0]) / HBM_PEAK_GBS, 4),
+                           "fp8_mfma_frac": round(idx_flops / (avg[0] * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4)},
+        "topk_transform": {"us": round(avg[1], 2), "us_median": round(med[1], 2), "bytes": topk_bytes,
+                           "GBps": round(gbs(topk_bytes, avg[1]), 1),
+                           "hbm_frac": round(gbs(topk_bytes, avg[1]) / HBM_PEAK_GBS, 4)},
+        "sparse_mla_decode": {"us": round(avg[2], 2), "us_median": round(med[2], 2), "bytes": mla_bytes,
+                              "GBps": round(gbs(mla_bytes, avg[2]), 1),
+                              "hbm_frac": round(gbs(mla_bytes, avg[2]) / HBM_PEAK_GBS, 4),
+                              "bf16_mfma_frac": round(mla_flops / (avg[2] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                              "num_splits": step.num_splits},
+    }
+    achieved = gbs(idx_bytes, avg[0])
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
+                "kernel": "indexer_logits_kernel<1>", "bytes_per_launch": idx_bytes,
+                "avg_launch_us": round(avg[0], 2)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(inp, kv, q_mla, lens, min(args.cpu_sample, B), scale, K)
+
+    print(json.dumps({
+        "metric": METRIC, "value": round(B / (ms_per_step * 1e-3), 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "us_per_step": round(ms_per_step * 1e3, 1), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8+bf16", "data": "synthetic",
+        "config": {"workload": "BASELINE config 2: full DSA decode step, one layer", "batch": B,
+                   "next_n": 1, "context_len": L, "index_topk": K, "indexer_heads": 64,
+                   "indexer_head_dim": 128, "mla_heads": H, "mla_dims": "576/512", "page_size": 64,
+                   "kv_cache": "fp8 656 B/token (block stride 65 rows)", "indexer_cache": "fp8 132 B/token",
+                   "parallelism": "single GPU"},
+        "roofline": roofline, "stages": stages, "cpu_baseline": cpu,
+    }), flush=True)
+
+
+if __name__ == "__main__":
+    main()
