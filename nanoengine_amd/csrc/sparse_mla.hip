@@ -5,23 +5,24 @@
 //   o   = softmax(s) @ kv(idx)[:, :512],  lse = log(sum_i exp(s_i))
 // where kv(slot) is a 656-byte row [512 e4m3fn][4 x f32 tile scale][64 bf16].
 //
-// Workgroup = 4 waves = 64 heads of one token over one key split. Per block of
-// 64 selected rows:
+// Workgroup = 4 waves = 64 heads of one token over one key split; each wave
+// owns 16 heads. Per block of 64 selected rows:
 //   load   : lane = row; wave w gathers tile w of the 64 rows (8 x 16 B fp8 +
-//            its f32 scale) and two 16 B rope chunks, one block ahead of use,
-//            so HBM latency hides behind the previous block's MFMAs;
+//            its f32 scale) and two 16 B rope chunks, two blocks ahead of use;
 //   stage  : rows are dequantised in registers (fp8 * 2^k is exact in bf16)
-//            and written to LDS twice: row-major Kb[64][576] for Q.K^T and
-//            transposed Vt[512][64] for P.V;
-//   QK     : wave w computes S^T[64 keys x 16 heads] with
-//            v_mfma_f32_16x16x32_bf16, A = Kb rows from LDS, B = its 16 query
-//            heads held in registers for the whole kernel (18 x 8 bf16);
-//   softmax: online (running max / sum in the exp2 domain), the max reduced
-//            across the four 16-lane groups with two shuffles;
-//   PV     : O^T[512 x 16 heads] += Vt . P^T, with P^T taken directly from the
-//            QK accumulators (no LDS round trip: the MFMA C layout of two
-//            16-key tiles is a key permutation of the B layout, and Vt is read
-//            with the same permutation).
+//            and written once, row-major, into one of two LDS buffers
+//            [64][576] bf16 (double buffering: one barrier per block);
+//   QK     : S^T[64 keys x 16 heads] on v_mfma_f32_16x16x32_bf16, A = rows
+//            from LDS (four independent accumulator chains), B = the wave's
+//            16 query heads, resident in registers for the whole kernel;
+//   softmax: online in the exp2 domain, with lazy rescaling: the running max
+//            only moves (and O is only rescaled) when a block raises it by
+//            more than 2^8, so P stays in [0, 256] and the rescale is rare;
+//   PV     : O[16 heads x 512] += P . V, A = P straight from the QK
+//            accumulators (two 16-key C tiles form one 32-key A operand), B =
+//            V read from the same row-major LDS tile with ds_read_b64_tr_b16,
+//            which hands each 16-lane group a transposed 4-key x 16-dv tile -
+//            no separate transposed copy of V.
 // Splits over the key list (for small batches) write normalised partial
 // outputs and LSEs to a caller-provided workspace; a combine kernel merges
 // them with the LSE rule of merge_attention_states.
@@ -32,19 +33,23 @@
 
 namespace dsa {
 
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
 constexpr int kMlaThreads = 256;
 constexpr int kMlaHeadsPerWG = 64;
-constexpr int kMlaKeys = 64;           // rows per block
+constexpr int kMlaKeys = 64;            // rows per block
 constexpr int kMlaRowBytes = 656;
 constexpr int kMlaDqk = 576;
 constexpr int kMlaDv = 512;
-constexpr int kKbPitch = kMlaDqk * 2 + 16;  // bytes per staged key row
-constexpr int kVtPitch = kMlaKeys * 2 + 16; // bytes per staged value column
-constexpr int kKbBytes = kMlaKeys * kKbPitch;
-constexpr int kVtBytes = kMlaDv * kVtPitch;
-constexpr size_t kMlaSmemBytes = (size_t)kKbBytes + kVtBytes;
+// Staged row pitch: 576 bf16 + 32 B. 296 dwords is an odd multiple of 8
+// banks, so 8 consecutive rows' 32-byte segments cover all 64 banks.
+constexpr int kPitch = kMlaDqk * 2 + 32;
+constexpr int kBufBytes = kMlaKeys * kPitch;
+constexpr size_t kMlaSmemBytes = 2 * (size_t)kBufBytes;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
 struct MlaParams {
   const uint16_t* q;
@@ -66,13 +71,14 @@ struct RowRegs {
   v4i nope[8];   // this wave's 128-dim tile of the lane's row
   v4i rope[2];   // rope chunks 2w, 2w+1
   float scale;
+  bool valid;
 };
 
 __device__ __forceinline__ void load_rows(RowRegs& rr, const MlaParams& P, int t, int key0, int lane,
-                                          int wave, bool& valid) {
+                                          int wave) {
   const int32_t slot = P.idx[(int64_t)t * P.idx_stride + key0 + lane];
-  valid = slot >= 0;
-  if (valid) {
+  rr.valid = slot >= 0;
+  if (rr.valid) {
     const uint8_t* row = P.kv + (int64_t)(slot / P.kv_block_size) * P.kv_blk_stride +
                          (int64_t)(slot % P.kv_block_size) * kMlaRowBytes;
     const v4i* nope = reinterpret_cast<const v4i*>(row + wave * 128);
@@ -92,8 +98,8 @@ __device__ __forceinline__ void load_rows(RowRegs& rr, const MlaParams& P, int t
   }
 }
 
-__device__ __forceinline__ void stage_rows(const RowRegs& rr, uint8_t* kb, uint8_t* vt, int lane, int wave) {
-  uint8_t* krow = kb + lane * kKbPitch;
+__device__ __forceinline__ void stage_rows(const RowRegs& rr, uint8_t* buf, int lane, int wave) {
+  uint8_t* krow = buf + lane * kPitch;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = wave * 8 + i;  // 16-dim chunk index, dims 16c .. 16c+15
@@ -101,14 +107,6 @@ __device__ __forceinline__ void stage_rows(const RowRegs& rr, uint8_t* kb, uint8
     dequant16_fp8_bf16(rr.nope[i], rr.scale, lo, hi);
     *reinterpret_cast<v4i*>(krow + c * 32) = lo;
     *reinterpret_cast<v4i*>(krow + c * 32 + 16) = hi;
-    uint16_t* vcol = reinterpret_cast<uint16_t*>(vt + (c * 16) * kVtPitch) + lane;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      vcol[(2 * e) * (kVtPitch / 2)] = (uint16_t)lo[e];
-      vcol[(2 * e + 1) * (kVtPitch / 2)] = (uint16_t)((uint32_t)lo[e] >> 16);
-      vcol[(8 + 2 * e) * (kVtPitch / 2)] = (uint16_t)hi[e];
-      vcol[(8 + 2 * e + 1) * (kVtPitch / 2)] = (uint16_t)((uint32_t)hi[e] >> 16);
-    }
   }
   *reinterpret_cast<v4i*>(krow + 1024 + wave * 32) = rr.rope[0];
   *reinterpret_cast<v4i*>(krow + 1024 + wave * 32 + 16) = rr.rope[1];
@@ -116,11 +114,19 @@ __device__ __forceinline__ void stage_rows(const RowRegs& rr, uint8_t* kb, uint8
 
 __device__ __forceinline__ v8bf as_v8bf(v4i x) { return __builtin_bit_cast(v8bf, x); }
 
+__device__ __forceinline__ int cvt_pk_bf16(float a, float b) {
+  const v2f x = {a, b};
+  return __builtin_bit_cast(int, __builtin_convertvector(x, v2bf));
+}
+
+__device__ __forceinline__ v4s lds_read_tr16(const uint8_t* p) {
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p);
+}
+
 __global__ void __launch_bounds__(kMlaThreads)
 sparse_mla_kernel(const MlaParams P) {
   extern __shared__ __align__(16) uint8_t smem[];
-  uint8_t* kb = smem;
-  uint8_t* vt = smem + kKbBytes;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
@@ -137,11 +143,12 @@ sparse_mla_kernel(const MlaParams P) {
   const int split = rem % P.splits;
   const int chunk = P.topk / P.splits;
   const int key_begin = split * chunk;
+  const int nblk = chunk / kMlaKeys;
 
   const int h0 = hg * kMlaHeadsPerWG + wave * 16;
   const bool active = h0 < P.H;
 
-  // Query heads as B operands: head h0 + lane%16, dims ks*32 + g*8 .. +8.
+  // Query heads as B operands of S^T = K . Q^T: head h0 + lane%16, dims ks*32 + g*8 .. +8.
   v4i qb[18];
   if (active) {
     const uint16_t* qh = P.q + (int64_t)t * P.q_tok_stride + (int64_t)(h0 + c16) * P.q_head_stride + g * 8;
@@ -149,118 +156,132 @@ sparse_mla_kernel(const MlaParams P) {
     for (int ks = 0; ks < 18; ++ks) qb[ks] = *reinterpret_cast<const v4i*>(qh + ks * 32);
   }
 
-  v4f acc[32];
+  // o[dt][r]: head h0 + 4g + r, dv dt*16 + c16
+  v4f o[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
-  float m_run = -__builtin_inff();
-  float l_run = 0.f;
+  for (int i = 0; i < 32; ++i) o[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+  float m_run = -__builtin_inff();  // per head c16, log2 domain
+  float l_run = 0.f;                // per head c16, this lane's keys only
 
   RowRegs rr;
-  bool valid;
-  load_rows(rr, P, t, key_begin, lane, wave, valid);
+  load_rows(rr, P, t, key_begin, lane, wave);
+  uint64_t vm_cur = __ballot(rr.valid);
+  stage_rows(rr, smem, lane, wave);
+  if (nblk > 1) load_rows(rr, P, t, key_begin + kMlaKeys, lane, wave);
+  __syncthreads();
 
-  for (int key0 = key_begin; key0 < key_begin + chunk; key0 += kMlaKeys) {
-    const uint64_t vmask = __ballot(valid);
-    __syncthreads();  // previous block's LDS reads are done
-    stage_rows(rr, kb, vt, lane, wave);
-    __syncthreads();
-    if (key0 + kMlaKeys < key_begin + chunk) load_rows(rr, P, t, key0 + kMlaKeys, lane, wave, valid);
-    if (!active || vmask == 0) continue;
-
-    // S^T tiles: s[kt][r] = score(key kt*16 + g*4 + r, head lane%16)
-    v4f s[4];
+  for (int n = 0; n < nblk; ++n) {
+    const uint8_t* buf = smem + (n & 1) * kBufBytes;
+    if (active && vm_cur) {
+      // ---- S^T = K . Q^T: s[kt][r] = score(key kt*16 + 4g + r, head c16)
+      v4f s[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      v4f c = {0.f, 0.f, 0.f, 0.f};
-      const uint8_t* arow = kb + (kt * 16 + c16) * kKbPitch + g * 16;
+      for (int kt = 0; kt < 4; ++kt) s[kt] = (v4f){0.f, 0.f, 0.f, 0.f};
+      const uint8_t* arow = buf + c16 * kPitch + g * 16;
 #pragma unroll
       for (int ks = 0; ks < 18; ++ks) {
-        const v4i a = *reinterpret_cast<const v4i*>(arow + ks * 64);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a), as_v8bf(qb[ks]), c, 0, 0, 0);
+        v4i a[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) a[kt] = *reinterpret_cast<const v4i*>(arow + kt * 16 * kPitch + ks * 64);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a[kt]), as_v8bf(qb[ks]), s[kt], 0, 0, 0);
       }
-      s[kt] = c;
-    }
 
-    float mloc = -__builtin_inff();
+      // ---- online softmax (exp2 domain), lazy rescale
+      float mloc = -__builtin_inff();
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kt * 16 + g * 4 + r;
-        const float x = ((vmask >> key) & 1ull) ? s[kt][r] * P.scale_log2 : -__builtin_inff();
-        s[kt][r] = x;
-        mloc = fmaxf(mloc, x);
+        for (int r = 0; r < 4; ++r) {
+          const int key = kt * 16 + g * 4 + r;
+          const float x = ((vm_cur >> key) & 1ull) ? s[kt][r] * P.scale_log2 : -__builtin_inff();
+          s[kt][r] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      mloc = fmaxf(mloc, shfl_xor(mloc, 16));
+      mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+      const bool need = mloc > m_run + kRescaleThreshold;  // true on the first valid block
+      if (__ballot(need)) {
+        const float m_new = need ? mloc : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
+        l_run *= alpha;
+        m_run = m_new;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha, g * 4 + r, 64);
+#pragma unroll
+          for (int dt = 0; dt < 32; ++dt) o[dt][r] *= ar;
+        }
       }
-    mloc = fmaxf(mloc, shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, shfl_xor(mloc, 32));
-    const float m_new = fmaxf(m_run, mloc);  // finite: vmask != 0
-    const float alpha = exp2f(m_run - m_new);
-    float psum = 0.f;
+      float psum = 0.f;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pv = exp2f(s[kt][r] - m_new);
-        s[kt][r] = pv;
-        psum += pv;
-      }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    if (__ballot(alpha != 1.f)) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) acc[i] *= alpha;
-    }
+        for (int r = 0; r < 4; ++r) {
+          const float pv = __builtin_amdgcn_exp2f(s[kt][r] - m_run);
+          s[kt][r] = pv;
+          psum += pv;
+        }
+      l_run += psum;
 
-    // P^T operands for the two 32-key steps.
-    v4i pb[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      pb[kk][0] = (int)pack_bf16_rne(s[2 * kk][0], s[2 * kk][1]);
-      pb[kk][1] = (int)pack_bf16_rne(s[2 * kk][2], s[2 * kk][3]);
-      pb[kk][2] = (int)pack_bf16_rne(s[2 * kk + 1][0], s[2 * kk + 1][1]);
-      pb[kk][3] = (int)pack_bf16_rne(s[2 * kk + 1][2], s[2 * kk + 1][3]);
-    }
-
-#pragma unroll
-    for (int dt = 0; dt < 32; ++dt) {
-      const uint8_t* vrow = vt + (dt * 16 + c16) * kVtPitch + g * 8;
+      // ---- O += P . V
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + kk * 64);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + kk * 64 + 32);
-        const v4i a = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a), as_v8bf(pb[kk]), acc[dt], 0, 0, 0);
+        v4i pa;
+        pa[0] = cvt_pk_bf16(s[2 * kk][0], s[2 * kk][1]);
+        pa[1] = cvt_pk_bf16(s[2 * kk][2], s[2 * kk][3]);
+        pa[2] = cvt_pk_bf16(s[2 * kk + 1][0], s[2 * kk + 1][1]);
+        pa[3] = cvt_pk_bf16(s[2 * kk + 1][2], s[2 * kk + 1][3]);
+        // lane (g, c16) addresses key row 32kk + 4g + c16/4 (and +16), dv 4*(c16%4) of each 16-dv tile
+        const uint8_t* v1 = buf + (32 * kk + 4 * g + (c16 >> 2)) * kPitch + (c16 & 3) * 8;
+        const uint8_t* v2 = v1 + 16 * kPitch;
+#pragma unroll
+        for (int dt = 0; dt < 32; ++dt) {
+          const v4s b1 = lds_read_tr16(v1 + dt * 32);
+          const v4s b2 = lds_read_tr16(v2 + dt * 32);
+          const v8bf b = __builtin_bit_cast(v8bf, __builtin_shufflevector(b1, b2, 0, 1, 2, 3, 4, 5, 6, 7));
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(pa), b, o[dt], 0, 0, 0);
+        }
       }
     }
+    uint64_t vm_next = 0;
+    if (n + 1 < nblk) {
+      vm_next = __ballot(rr.valid);
+      stage_rows(rr, smem + ((n + 1) & 1) * kBufBytes, lane, wave);
+    }
+    if (n + 2 < nblk) load_rows(rr, P, t, key_begin + (n + 2) * kMlaKeys, lane, wave);
+    __syncthreads();
+    vm_cur = vm_next;
   }
 
   if (!active) return;
   l_run += shfl_xor(l_run, 16);
   l_run += shfl_xor(l_run, 32);
-  const int h = h0 + c16;
   const bool any = l_run > 0.f;
   const float inv = any ? 1.f / l_run : 0.f;
-  const float lse = any ? (m_run + log2f(l_run)) * kLn2 : -__builtin_inff();
+  const float lse = any ? (m_run + __builtin_amdgcn_logf(l_run)) * kLn2 : -__builtin_inff();
+  float inv_r[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) inv_r[r] = __shfl(inv, g * 4 + r, 64);
 
   if (P.splits == 1) {
-    uint16_t* o = P.out + ((int64_t)t * P.H + h) * kMlaDv + g * 4;
 #pragma unroll
-    for (int dt = 0; dt < 32; ++dt) {
-      uint2 v;
-      v.x = pack_bf16_rne(acc[dt][0] * inv, acc[dt][1] * inv);
-      v.y = pack_bf16_rne(acc[dt][2] * inv, acc[dt][3] * inv);
-      *reinterpret_cast<uint2*>(o + dt * 16) = v;
+    for (int r = 0; r < 4; ++r) {
+      uint16_t* orow = P.out + ((int64_t)t * P.H + h0 + g * 4 + r) * kMlaDv + c16;
+#pragma unroll
+      for (int dt = 0; dt < 32; ++dt) orow[dt * 16] = (uint16_t)f32_to_bf16_rne(o[dt][r] * inv_r[r]);
     }
-    if (g == 0 && P.lse) P.lse[(int64_t)t * P.H + h] = lse;
+    if (g == 0 && P.lse) P.lse[(int64_t)t * P.H + h0 + c16] = lse;
   } else {
-    const int64_t row = ((int64_t)split * P.T + t) * P.H + h;
-    float* o = P.ws_o + row * kMlaDv + g * 4;
+    const int64_t row0 = ((int64_t)split * P.T + t) * P.H + h0;
 #pragma unroll
-    for (int dt = 0; dt < 32; ++dt) {
-      v4f v = acc[dt] * inv;
-      *reinterpret_cast<v4f*>(o + dt * 16) = v;
+    for (int r = 0; r < 4; ++r) {
+      float* orow = P.ws_o + (row0 + g * 4 + r) * kMlaDv + c16;
+#pragma unroll
+      for (int dt = 0; dt < 32; ++dt) orow[dt * 16] = o[dt][r] * inv_r[r];
     }
-    if (g == 0) P.ws_lse[row] = lse;
+    if (g == 0) P.ws_lse[row0 + c16] = lse;
   }
 }
 
