@@ -48,6 +48,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample")
     p.add_argument("--copy-calib", action="store_true")
+    p.add_argument("--only", choices=["indexer", "topk", "mla"], default=None,
+                   help="profiling aid: launch only this stage in the timed loop (no JSON line)")
     return p.parse_args()
 
 
@@ -150,6 +152,23 @@ def main():
                               num_splits=step.num_splits, workspace=step.workspace)
         if ev is not None:
             ev[3].record()
+
+    if args.only:
+        from nanoengine_amd import ops
+        run()
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            if args.only == "indexer":
+                ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+                                   max_ctx, out=step.logits)
+            elif args.only == "topk":
+                ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical)
+            else:
+                ops.sparse_mla_decode(q_mla, kv, step.physical, scale, out=step.out, lse=step.lse,
+                                      num_splits=step.num_splits, workspace=step.workspace)
+        torch.cuda.synchronize()
+        print(f"ran {args.steps} launches of {args.only}", flush=True)
+        return
 
     for _ in range(args.warmup):
         run()

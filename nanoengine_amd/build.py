@@ -25,8 +25,11 @@ HIPCC_FLAGS = [
     "-fvisibility=hidden",
     "-Wall",
     "-Wno-unused-result",
-    # No packed-fp32 instructions in device code (see the HIP code notes).
+    # No packed-fp32 instructions in device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the accumulators feed VALU work (ReLU, softmax,
+    # rescale) every block, and AGPR-resident results cost a copy each time.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

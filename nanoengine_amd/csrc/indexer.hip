@@ -11,8 +11,8 @@
 // the head weights are applied on the fp32 accumulators, and a 3-shuffle
 // butterfly finishes the head sum so that lane l ends up owning token l of the
 // page: the logits row segment and the per-token scales are then one
-// coalesced 256-byte load/store each. The next page's keys are loaded before
-// the current page's MFMAs so that HBM latency overlaps compute.
+// coalesced 256-byte load/store each. Each wave keeps two pages in flight
+// (three rotating register buffers) so that HBM latency overlaps compute.
 //
 // Page layout (bytes): [64 tokens x 128 fp8][64 x f32 scale] = 8448.
 #include "dsa_common.h"
@@ -22,7 +22,7 @@ namespace dsa {
 
 constexpr int kIdxThreads = 256;
 constexpr int kIdxWaves = kIdxThreads / 64;
-constexpr int kIdxPagesPerWave = 8;
+constexpr int kIdxPagesPerWave = 6;
 constexpr int kIdxPageTokens = 64;
 constexpr int kIdxHeadDim = 128;
 constexpr int kIdxHeads = 64;
@@ -37,6 +37,9 @@ __device__ __forceinline__ v8i load32B(const uint8_t* p) {
   return r;
 }
 
+// max(x, 0) in one instruction (v_med3_f32 with bounds 0 and FLT_MAX).
+__device__ __forceinline__ float relu(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, 3.402823466e38f); }
+
 struct PageRegs {
   v8i k[4];      // token tiles: lane holds token tt*16 + lane%16, bytes (lane/16)*32 .. +32
   float scale;   // scale of token `lane`
@@ -50,7 +53,63 @@ __device__ __forceinline__ void load_page(PageRegs& pr, const uint8_t* page, int
 }
 
 template <int NQ>
-__global__ void __launch_bounds__(kIdxThreads)
+__device__ __forceinline__ void compute_page(const PageRegs& cur, int p, int lane, const v8i (&qa)[NQ][4],
+                                             const float (&w)[NQ][4][4], const int (&L)[NQ], int64_t max_ctx,
+                                             float* __restrict__ logits, int64_t logits_stride, int b) {
+#ifdef DSA_IDX_EXPERIMENT_NO_COMPUTE
+  {
+    v8i x = cur.k[0] ^ cur.k[1] ^ cur.k[2] ^ cur.k[3];
+    const int t = p * kIdxPageTokens + lane;
+    const int xx = x[0] ^ x[1] ^ x[2] ^ x[3] ^ x[4] ^ x[5] ^ x[6] ^ x[7];
+#ifdef DSA_IDX_EXPERIMENT_NO_STORE
+    if (xx == 0x12345 && t < max_ctx)
+#else
+    if (t < max_ctx)
+#endif
+      logits[(int64_t)b * NQ * logits_stride + t] = (float)xx * cur.scale;
+    return;
+  }
+#endif
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    float part[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      // four independent products per token tile keep the MFMA pipe busy
+      v4f c[4];
+#pragma unroll
+      for (int ht = 0; ht < 4; ++ht)
+        c[ht] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j][ht], cur.k[tt], (v4f){0.f, 0.f, 0.f, 0.f},
+                                                                0, 0, 0, 127, 0, 127);
+      // c[ht][r]: head ht*16 + (lane/16)*4 + r, token tt*16 + lane%16
+      float acc = 0.f;
+#pragma unroll
+      for (int ht = 0; ht < 4; ++ht)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc = fmaf(w[j][ht][r], relu(c[ht][r]), acc);
+      part[tt] = acc;
+    }
+    // Butterfly over the four 16-lane groups: lane group g keeps token tile g.
+    const bool hi32 = lane & 32;
+    const float s0 = hi32 ? part[0] : part[2];
+    const float s1 = hi32 ? part[1] : part[3];
+    const float k0 = (hi32 ? part[2] : part[0]) + shfl_xor(s0, 32);
+    const float k1 = (hi32 ? part[3] : part[1]) + shfl_xor(s1, 32);
+    const bool hi16 = lane & 16;
+    const float v = (hi16 ? k1 : k0) + shfl_xor(hi16 ? k0 : k1, 16);
+    const int t = p * kIdxPageTokens + lane;
+    if (t < max_ctx) {
+      float* dst = logits + (int64_t)(b * NQ + j) * logits_stride;
+      // streaming store: the logits are consumed by a later kernel, not reused here
+      __builtin_nontemporal_store(t < L[j] ? v * cur.scale : -__builtin_inff(), dst + t);
+    }
+  }
+}
+
+// Two waves per SIMD: three 33-VGPR page buffers, the resident query tiles
+// and head weights take ~180 VGPRs for one query token.
+template <int NQ>
+__global__ void __launch_bounds__(kIdxThreads) __attribute__((amdgpu_waves_per_eu(2)))
 indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
                       const float* __restrict__ weights, const int32_t* __restrict__ ctx_lens,
                       const int32_t* __restrict__ block_tables, int64_t bt_stride, int64_t max_ctx,
@@ -85,47 +144,26 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
   }
 
   const int32_t* bt = block_tables + (int64_t)b * bt_stride;
-  PageRegs cur, nxt;
-  int p = p_begin;
-  if (p < npages) load_page(cur, kv + (int64_t)bt[p] * kIdxPageBytes, lane);
-
-  for (int it = 0; it < kIdxPagesPerWave && p < npages; ++it) {
-    const int pn = p + kIdxWaves;
-    const bool has_next = (it + 1 < kIdxPagesPerWave) && pn < npages;
-    if (has_next) load_page(nxt, kv + (int64_t)bt[pn] * kIdxPageBytes, lane);
-
+  // Three page buffers rotate so that two pages are in flight while one is
+  // being multiplied; the wave's pages are p_begin + 4*i.
+  PageRegs buf0, buf1, buf2;
+  auto valid = [&](int i) { return i < kIdxPagesPerWave && p_begin + kIdxWaves * i < npages; };
+  // All of the wave's block-table entries in one load up front, so no page
+  // load waits behind a dependent table read.
+  const int my_page = (lane < kIdxPagesPerWave && valid(lane)) ? bt[p_begin + kIdxWaves * lane] : 0;
+  auto page_ptr = [&](int i) {
+    return kv + (int64_t)__builtin_amdgcn_readlane(my_page, i) * kIdxPageBytes;
+  };
+  if (valid(0)) load_page(buf0, page_ptr(0), lane);
+  if (valid(1)) load_page(buf1, page_ptr(1), lane);
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      float part[4];
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        float acc = 0.f;
-#pragma unroll
-        for (int ht = 0; ht < 4; ++ht) {
-          v4f c = {0.f, 0.f, 0.f, 0.f};
-          c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j][ht], cur.k[tt], c, 0, 0, 0, 127, 0, 127);
-          // c[r]: head ht*16 + (lane/16)*4 + r, token tt*16 + lane%16
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc = fmaf(w[j][ht][r], fmaxf(c[r], 0.f), acc);
-        }
-        part[tt] = acc;
-      }
-      // Butterfly over the four 16-lane groups: lane group g keeps token tile g.
-      const bool hi32 = lane & 32;
-      const float s0 = hi32 ? part[0] : part[2];
-      const float s1 = hi32 ? part[1] : part[3];
-      const float k0 = (hi32 ? part[2] : part[0]) + shfl_xor(s0, 32);
-      const float k1 = (hi32 ? part[3] : part[1]) + shfl_xor(s1, 32);
-      const bool hi16 = lane & 16;
-      const float v = (hi16 ? k1 : k0) + shfl_xor(hi16 ? k0 : k1, 16);
-      const int t = p * kIdxPageTokens + lane;
-      if (t < max_ctx) {
-        float* dst = logits + (int64_t)(b * NQ + j) * logits_stride;
-        dst[t] = t < L[j] ? v * cur.scale : -__builtin_inff();
-      }
-    }
-    if (has_next) cur = nxt;
-    p = pn;
+  for (int i = 0; i < kIdxPagesPerWave; i += 3) {
+    if (valid(i + 2)) load_page(buf2, page_ptr(i + 2), lane);
+    if (valid(i)) compute_page<NQ>(buf0, p_begin + kIdxWaves * i, lane, qa, w, L, max_ctx, logits, logits_stride, b);
+    if (valid(i + 3)) load_page(buf0, page_ptr(i + 3), lane);
+    if (valid(i + 1)) compute_page<NQ>(buf1, p_begin + kIdxWaves * (i + 1), lane, qa, w, L, max_ctx, logits, logits_stride, b);
+    if (valid(i + 4)) load_page(buf1, page_ptr(i + 4), lane);
+    if (valid(i + 2)) compute_page<NQ>(buf2, p_begin + kIdxWaves * (i + 2), lane, qa, w, L, max_ctx, logits, logits_stride, b);
   }
 }
 
