@@ -145,7 +145,7 @@ def main():
                            max_ctx, out=step.logits)
         if ev is not None:
             ev[1].record()
-        ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical)
+        ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical, workspace=step.topk_workspace)
         if ev is not None:
             ev[2].record()
         ops.sparse_mla_decode(q_mla, kv, step.physical, scale, out=step.out, lse=step.lse,
@@ -162,7 +162,7 @@ def main():
                 ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
                                    max_ctx, out=step.logits)
             elif args.only == "topk":
-                ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical)
+                ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical, workspace=step.topk_workspace)
             else:
                 ops.sparse_mla_decode(q_mla, kv, step.physical, scale, out=step.out, lse=step.lse,
                                       num_splits=step.num_splits, workspace=step.workspace)

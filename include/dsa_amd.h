@@ -79,6 +79,10 @@ DSA_API int dsa_indexer_logits(const uint8_t* q_fp8, const uint8_t* kv_cache,
                        int page_size, int64_t max_context_len,
                        float* logits, int64_t logits_stride, void* stream);
 
+/* Workspace bytes the top-k entry points use for `batch` rows (per-row
+ * threshold, counter and a 4096-entry candidate list: 32 KB + 16 B a row). */
+DSA_API size_t dsa_topk_workspace_bytes(int batch);
+
 /* Exact top-k selection with page-table translation.
  *   scores          [batch, >= seq_lens[b]] f32, row stride `score_stride`
  *   seq_lens        [batch] int32
@@ -86,6 +90,9 @@ DSA_API int dsa_indexer_logits(const uint8_t* q_fp8, const uint8_t* kv_cache,
  *                   then out_page receives the raw positions (no translation)
  *   out_page        [batch, top_k] int32, contiguous
  *   out_raw         [batch, top_k] int32 or NULL
+ *   workspace       >= dsa_topk_workspace_bytes(batch) bytes, 16-byte aligned,
+ *                   or NULL (then every row takes the slower multi-pass path;
+ *                   the result is the same)
  * Row b selects the top_k largest scores among positions [0, seq_lens[b])
  * (ties: lowest positions; NaN ranks as -inf), writes them in ascending
  * position order as raw positions and as slots
@@ -93,26 +100,29 @@ DSA_API int dsa_indexer_logits(const uint8_t* q_fp8, const uint8_t* kv_cache,
  * then pads with -1. seq_lens[b] <= top_k emits 0..seq_lens[b]-1.
  * top_k in {512, 2048}; page_size a power of two;
  * row length <= dsa_topk_max_len(); `max_len` bounds seq_lens (the score width).
+ * Calls that share a workspace must be ordered (same stream).
  * Replaces topk_transform(scores, seq_lens, page_tables, out_page_indices,
  * page_size, top_k, out_raw_indices)
  * (dlengine/runtime/kernel/jit/sgl/deepseek_v4.py:324-367,
  *  kernel csrc/deepseek_v4/topk.cuh:249-287, host TopKKernel::transform :336-394). */
 DSA_API int dsa_topk_transform(const float* scores, int64_t score_stride,
-                       const int32_t* seq_lens, const int32_t* page_table,
-                       int64_t page_table_stride, int32_t* out_page,
-                       int32_t* out_raw, int batch, int64_t max_len,
-                       int page_size, int top_k, void* stream);
+                               const int32_t* seq_lens, const int32_t* page_table,
+                               int64_t page_table_stride, int32_t* out_page,
+                               int32_t* out_raw, int batch, int64_t max_len,
+                               int page_size, int top_k, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* Ragged exact top-k: row b selects among scores[b, row_starts[b] +
  * [0, seq_lens[b])] and writes position + offsets[b], ascending, padded -1.
  * top_k == 2048. Exact (the reference's bounded candidate buffer allows a few
- * differences; this kernel has none).
+ * differences; this kernel has none). Workspace as for dsa_topk_transform.
  * Replaces topk_transform_ragged(scores, seq_lens, row_starts, offsets,
  * out_indices, top_k) (deepseek_v4.py:370-388, topk.cuh:289-316). */
 DSA_API int dsa_topk_transform_ragged(const float* scores, int64_t score_stride,
-                              const int32_t* seq_lens, const int32_t* row_starts,
-                              const int32_t* offsets, int32_t* out,
-                              int batch, int64_t max_len, int top_k, void* stream);
+                                      const int32_t* seq_lens, const int32_t* row_starts,
+                                      const int32_t* offsets, int32_t* out,
+                                      int batch, int64_t max_len, int top_k,
+                                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Logical token positions -> physical cache slots.
  *   topk_indices [rows, topk] int32, row stride `topk_stride` (-1 = padding)

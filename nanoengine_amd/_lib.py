@@ -21,8 +21,11 @@ SIGNATURES = {
     "dsa_indexer_schedule": (c_int, [_P, c_int, c_int, c_int, _P, _P]),
     "dsa_indexer_logits": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, c_int,
                                    c_int64, _P, c_int64, _P]),
-    "dsa_topk_transform": (c_int, [_P, c_int64, _P, _P, c_int64, _P, _P, c_int, c_int64, c_int, c_int, _P]),
-    "dsa_topk_transform_ragged": (c_int, [_P, c_int64, _P, _P, _P, _P, c_int, c_int64, c_int, _P]),
+    "dsa_topk_workspace_bytes": (c_size_t, [c_int]),
+    "dsa_topk_transform": (c_int, [_P, c_int64, _P, _P, c_int64, _P, _P, c_int, c_int64, c_int, c_int, _P,
+                                   c_size_t, _P]),
+    "dsa_topk_transform_ragged": (c_int, [_P, c_int64, _P, _P, _P, _P, c_int, c_int64, c_int, _P, c_size_t,
+                                          _P]),
     "dsa_topk_to_physical": (c_int, [_P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, c_int, _P, _P]),
     "dsa_sparse_mla_num_splits": (c_int, [c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),

@@ -56,20 +56,6 @@ template <int NQ>
 __device__ __forceinline__ void compute_page(const PageRegs& cur, int p, int lane, const v8i (&qa)[NQ][4],
                                              const float (&w)[NQ][4][4], const int (&L)[NQ], int64_t max_ctx,
                                              float* __restrict__ logits, int64_t logits_stride, int b) {
-#ifdef DSA_IDX_EXPERIMENT_NO_COMPUTE
-  {
-    v8i x = cur.k[0] ^ cur.k[1] ^ cur.k[2] ^ cur.k[3];
-    const int t = p * kIdxPageTokens + lane;
-    const int xx = x[0] ^ x[1] ^ x[2] ^ x[3] ^ x[4] ^ x[5] ^ x[6] ^ x[7];
-#ifdef DSA_IDX_EXPERIMENT_NO_STORE
-    if (xx == 0x12345 && t < max_ctx)
-#else
-    if (t < max_ctx)
-#endif
-      logits[(int64_t)b * NQ * logits_stride + t] = (float)xx * cur.scale;
-    return;
-  }
-#endif
 #pragma unroll
   for (int j = 0; j < NQ; ++j) {
     float part[4];

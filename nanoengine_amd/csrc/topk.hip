@@ -1,29 +1,35 @@
 // Exact top-k selection (+ page-table translation) and the logical->physical
 // index transform for the DSA decode path, written for gfx950.
 //
-// Selection is a most-significant-digit radix select on a 50-bit composite key
+// Order: a most-significant-digit radix select on a 50-bit composite key
 //   [ order_key(score) : 32 bits ][ (2^18-1) - position : 18 bits ]
 // so that every element is distinct and equal scores resolve to the lowest
-// positions. Digits are 12/10/10 bits of the score key and 9/9 bits of the
-// inverted position. One 1024-thread workgroup owns one row:
-//   1. one pass over the row in HBM builds the 4096-bin histogram of digit 0;
-//   2. each level finds the threshold bin with a block suffix scan, marks every
-//      element above it in an LDS bitmap (one bit per position), and gathers the
-//      threshold bin's elements for the next digit - into an LDS candidate list
-//      when they fit (4096 entries), otherwise by another filtered pass over
-//      the row, so the result is exact for any distribution (no bounded
-//      candidate buffer, unlike the reference's 16K limit);
-//   3. the bitmap is compacted with one block prefix scan, which emits the
-//      selected positions in ascending order (deterministic output), and the
-//      page-table translation is applied while writing.
-// Typical rows need two HBM passes (histogram, mark+gather) and no global sort.
+// positions (NaN ranks as -inf). Digits are 12/10/10 bits of the score key and
+// 9/9 bits of the inverted position.
+//
+// One call is three launches on the caller's stream:
+//   1. threshold (one workgroup per row): a 1/8 sample of the row (contiguous
+//      1024-element chunks, one in eight) gives, by a two-digit radix on the
+//      sample, a score threshold t with about k + 4 sqrt(k) elements expected
+//      at or above it - a bound that holds with a wide margin;
+//   2. gather (8192 positions per workgroup, 8 per 64K row): one coalesced
+//      read of the scores, one compare per element, and the elements at or
+//      above t are appended - (key, position) - to the row's candidate list in
+//      the workspace (wave ballots into LDS, one global atomic per workgroup);
+//   3. finish (one workgroup per row): if the list holds between k and its
+//      capacity entries, the exact top-k of the row is the exact top-k of the
+//      list, found by radix levels in LDS; otherwise the row falls back to
+//      the full exact select, which re-reads the row from HBM per level and
+//      needs no bound at all. The selected positions are marked in an LDS
+//      bitmap, compacted with one block prefix scan (ascending order, so the
+//      output is deterministic) and written with the page translation.
+// No global sort, no bounded candidate buffer on the exact path.
 #include "dsa_common.h"
 #include "../../include/dsa_amd.h"
 
 namespace dsa {
 
-constexpr int kTopkThreads = 1024;
-constexpr int kTopkWaves = kTopkThreads / 64;
+constexpr int kTopkThreads = 512;
 constexpr int kTopkMaxLen = 1 << 18;            // positions per row
 constexpr int kBitmapWords = kTopkMaxLen / 32;  // 32 KB of LDS
 constexpr int kListCap = 4096;                  // candidates per list buffer
@@ -31,12 +37,29 @@ constexpr int kHistBins = 4096;
 constexpr uint32_t kIdxMax = (1u << 18) - 1;
 constexpr int kLevels = 5;
 
+// threshold / gather geometry
+constexpr int kAuxThreads = 256;
+constexpr int kSampleChunk = 1024;              // contiguous sampled chunk
+constexpr int kSampleEvery = 8;                 // one chunk in eight
+constexpr int kGatherPerThread = 32;
+constexpr int kGatherSpan = kAuxThreads * kGatherPerThread;  // 8192 positions per workgroup
+constexpr int kGatherLdsCap = 2048;             // candidates one gather workgroup can stage
+
+// Per-row workspace: header [t_key, count, pad, pad] then the candidate list.
+struct RowWs {
+  uint32_t t_key;
+  uint32_t count;
+  uint32_t pad[2];
+  uint32_t key[kListCap];
+  uint32_t pos[kListCap];
+};
+
 struct TopkSmem {
   uint32_t hist[kHistBins];
   uint32_t bitmap[kBitmapWords];
   uint32_t list_key[2][kListCap];
   uint32_t list_pos[2][kListCap];
-  uint32_t wave_sum[kTopkWaves];
+  uint32_t wave_sum[16];
   uint32_t list_count[2];
   uint32_t tb, above, eq;
 };
@@ -68,15 +91,24 @@ __device__ __forceinline__ bool in_bucket(int level, uint32_t key, uint32_t pos,
   }
 }
 
-// Block-wide: find the bin tb with S(tb+1) < remain <= S(tb), S(b) = sum of
-// hist[b..nbins). Leaves tb, above = S(tb+1), eq = hist[tb] in shared memory.
-__device__ void find_threshold(TopkSmem& s, int nbins, uint32_t remain) {
+// Inverse of order_key: the float whose key is k.
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+
+// Block-wide (NT threads): find the bin tb with S(tb+1) < remain <= S(tb),
+// S(b) = sum of hist[b..nbins). Leaves tb, above = S(tb+1), eq = hist[tb] in
+// the shared *tb_out, *above_out, *eq_out for every thread after the call.
+template <int NT>
+__device__ void find_threshold(const uint32_t* hist, uint32_t* wave_sum, int nbins, uint32_t remain,
+                               uint32_t* tb_out, uint32_t* above_out, uint32_t* eq_out) {
+  constexpr int kWaves = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int per = nbins >= kTopkThreads ? nbins / kTopkThreads : 1;
+  const int per = nbins >= NT ? nbins / NT : 1;
   const int first = tid * per;
   uint32_t local = 0;
   if (first < nbins)
-    for (int i = 0; i < per; ++i) local += s.hist[first + i];
+    for (int i = 0; i < per; ++i) local += hist[first + i];
   // inclusive suffix sum inside the wave
   uint32_t v = local;
 #pragma unroll
@@ -84,18 +116,18 @@ __device__ void find_threshold(TopkSmem& s, int nbins, uint32_t remain) {
     uint32_t n = __shfl_down(v, off, 64);
     if (lane + off < 64) v += n;
   }
-  if (lane == 0) s.wave_sum[wave] = v;
+  if (lane == 0) wave_sum[wave] = v;
   __syncthreads();
   uint32_t higher = v - local;
-  for (int w = wave + 1; w < kTopkWaves; ++w) higher += s.wave_sum[w];
+  for (int w = wave + 1; w < kWaves; ++w) higher += wave_sum[w];
   if (first < nbins) {
     uint32_t acc = higher;
     for (int i = per - 1; i >= 0; --i) {
-      uint32_t h = s.hist[first + i];
+      uint32_t h = hist[first + i];
       if (acc < remain && acc + h >= remain) {
-        s.tb = first + i;
-        s.above = acc;
-        s.eq = h;
+        *tb_out = first + i;
+        *above_out = acc;
+        *eq_out = h;
       }
       acc += h;
     }
@@ -105,7 +137,9 @@ __device__ void find_threshold(TopkSmem& s, int nbins, uint32_t remain) {
 
 // Exclusive block prefix sum of one value per thread; returns the prefix and
 // writes the block total to *total (all threads).
-__device__ uint32_t block_exclusive_scan(TopkSmem& s, uint32_t x, uint32_t* total) {
+template <int NT>
+__device__ uint32_t block_exclusive_scan(uint32_t* wave_sum, uint32_t x, uint32_t* total) {
+  constexpr int kWaves = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t v = x;
 #pragma unroll
@@ -114,11 +148,11 @@ __device__ uint32_t block_exclusive_scan(TopkSmem& s, uint32_t x, uint32_t* tota
     if (lane >= off) v += n;
   }
   __syncthreads();
-  if (lane == 63) s.wave_sum[wave] = v;
+  if (lane == 63) wave_sum[wave] = v;
   __syncthreads();
   uint32_t before = 0, all = 0;
-  for (int w = 0; w < kTopkWaves; ++w) {
-    uint32_t t = s.wave_sum[w];
+  for (int w = 0; w < kWaves; ++w) {
+    uint32_t t = wave_sum[w];
     if (w < wave) before += t;
     all += t;
   }
@@ -127,9 +161,9 @@ __device__ uint32_t block_exclusive_scan(TopkSmem& s, uint32_t x, uint32_t* tota
 }
 
 struct RowOut {
-  int32_t* page;       // page-translated output (or the ragged output)
+  int32_t* page;       // page-translated output (or the untranslated output)
   int32_t* raw;        // optional raw positions
-  const int32_t* pt;   // page table row (NULL for ragged)
+  const int32_t* pt;   // page table row (NULL: write positions + offset)
   uint32_t page_bits;
   int32_t offset;      // ragged offset
   __device__ __forceinline__ void emit(int slot, int32_t p) const {
@@ -147,22 +181,160 @@ struct RowOut {
   }
 };
 
+struct RowIn {
+  const float* scores;
+  int64_t stride;
+  const int32_t* seq_lens;
+  const int32_t* row_starts;
+  int64_t max_len;
+  __device__ __forceinline__ int len(int b) const {
+    int64_t l = seq_lens[b];
+    return (int)(l < 0 ? 0 : (l > max_len ? max_len : l));
+  }
+  __device__ __forceinline__ const float* row(int b) const {
+    return scores + (int64_t)b * stride + (row_starts ? row_starts[b] : 0);
+  }
+};
+
+// ---------------------------------------------------------------- 1. threshold
+__global__ void __launch_bounds__(kAuxThreads)
+topk_threshold_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
+  __shared__ uint32_t hist[kHistBins];
+  __shared__ uint32_t wave_sum[kAuxThreads / 64];
+  __shared__ uint32_t tb, above, eq;
+  const int tid = threadIdx.x, b = blockIdx.x;
+  const int len = in.len(b);
+  RowWs& w = ws[b];
+  if (len <= top_k) {
+    if (tid == 0) { w.t_key = 0u; w.count = 0u; }
+    return;
+  }
+  const float* row = in.row(b);
+  for (int i = tid; i < kHistBins; i += kAuxThreads) hist[i] = 0u;
+  __syncthreads();
+  // sampled chunks start at multiples of kSampleChunk * kSampleEvery
+  constexpr int kStride = kSampleChunk * kSampleEvery;
+  const int nchunks = (len + kStride - 1) / kStride;
+  for (int c0 = 0; c0 < nchunks; c0 += 8) {
+    float x[8][4];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int pos = (c0 + c) * kStride + e * kAuxThreads + tid;
+        x[c][e] = (c0 + c < nchunks && pos < len) ? row[pos] : 0.f;
+      }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int pos = (c0 + c) * kStride + e * kAuxThreads + tid;
+        if (c0 + c < nchunks && pos < len) atomicAdd(&hist[order_key(x[c][e]) >> 20], 1u);
+      }
+  }
+  uint32_t nsample = 0;
+  for (int c = 0; c < nchunks; ++c) nsample += (uint32_t)max(0, min(len - c * kStride, kSampleChunk));
+  const float fk = (float)nsample / (float)len * (float)top_k;
+  const uint32_t r = (uint32_t)(fk + 4.f * sqrtf(fk) + 8.f);
+  __syncthreads();
+  uint32_t t_key = 0u;  // 0: gather everything
+  if (r < nsample) {
+    find_threshold<kAuxThreads>(hist, wave_sum, 4096, r, &tb, &above, &eq);
+    const uint32_t tb0 = tb, rem0 = r - above;
+    __syncthreads();
+    for (int i = tid; i < 1024; i += kAuxThreads) hist[i] = 0u;
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int pos = c * kStride + e * kAuxThreads + tid;
+        if (pos < len) {
+          const uint32_t k = order_key(row[pos]);  // second look at the sample: L2 hits
+          if ((k >> 20) == tb0) atomicAdd(&hist[(k >> 10) & 1023u], 1u);
+        }
+      }
+    __syncthreads();
+    find_threshold<kAuxThreads>(hist, wave_sum, 1024, rem0, &tb, &above, &eq);
+    t_key = (tb0 << 20) | (tb << 10);
+  }
+  if (tid == 0) {
+    w.t_key = t_key;
+    w.count = 0u;
+  }
+}
+
+// ---------------------------------------------------------------- 2. gather
+__global__ void __launch_bounds__(kAuxThreads)
+topk_gather_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
+  __shared__ uint32_t s_key[kGatherLdsCap];
+  __shared__ uint32_t s_pos[kGatherLdsCap];
+  __shared__ uint32_t s_count, s_base;
+  const int tid = threadIdx.x, lane = tid & 63, b = blockIdx.y;
+  const int len = in.len(b);
+  const int span0 = blockIdx.x * kGatherSpan;
+  if (len <= top_k || span0 >= len) return;
+  const float* row = in.row(b);
+  RowWs& w = ws[b];
+  if (tid == 0) s_count = 0u;
+  const uint32_t t_key = w.t_key;
+  // -inf and NaN share the lowest key; at or below it every element is gathered
+  const bool all = t_key <= order_key(-__builtin_inff());
+  const float t_f = key_to_float(t_key);
+  float x[kGatherPerThread];
+#pragma unroll
+  for (int j = 0; j < kGatherPerThread; ++j) {
+    const int pos = span0 + j * kAuxThreads + tid;
+    x[j] = pos < len ? __builtin_nontemporal_load(row + pos) : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kGatherPerThread; ++j) {
+    const int pos = span0 + j * kAuxThreads + tid;
+    // the float compare admits every key >= t_key (and -0.0 against +0.0,
+    // which only adds a candidate)
+    const bool pred = pos < len && (all || x[j] >= t_f);
+    const uint64_t m = __ballot(pred);
+    if (m) {
+      const int leader = __builtin_ctzll(m);
+      uint32_t base = 0;
+      if (lane == leader) base = atomicAdd(&s_count, (uint32_t)__popcll(m));
+      base = __shfl(base, leader, 64);
+      if (pred) {
+        const uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+        if (slot < kGatherLdsCap) {
+          s_key[slot] = order_key(x[j]);
+          s_pos[slot] = (uint32_t)pos;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t n = s_count;
+  if (tid == 0) {
+    // an overflowing workgroup poisons the count so that the row falls back
+    s_base = n ? atomicAdd(&w.count, n > kGatherLdsCap ? (uint32_t)(kListCap + 1) : n) : 0u;
+  }
+  __syncthreads();
+  const uint32_t base = s_base;
+  if (n <= kGatherLdsCap)
+    for (uint32_t e = tid; e < n; e += kAuxThreads)
+      if (base + e < kListCap) {
+        w.key[base + e] = s_key[e];
+        w.pos[base + e] = s_pos[e];
+      }
+}
+
+// ---------------------------------------------------------------- 3. finish
 __global__ void __launch_bounds__(kTopkThreads)
-topk_select_kernel(const float* __restrict__ scores, int64_t score_stride,
-                   const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ row_starts,
-                   const int32_t* __restrict__ offsets, const int32_t* __restrict__ page_table,
-                   int64_t pt_stride, uint32_t page_bits, int32_t* __restrict__ out_page,
-                   int32_t* __restrict__ out_raw, int64_t max_len, int top_k) {
+topk_finish_kernel(const RowIn in, const RowWs* __restrict__ ws, const int32_t* __restrict__ offsets,
+                   const int32_t* __restrict__ page_table, int64_t pt_stride, uint32_t page_bits,
+                   int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   TopkSmem& s = *reinterpret_cast<TopkSmem*>(smem_raw);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int b = blockIdx.x;
-
-  int64_t len64 = seq_lens[b];
-  if (len64 < 0) len64 = 0;
-  if (len64 > max_len) len64 = max_len;
-  const int len = (int)len64;
-  const float* row = scores + (int64_t)b * score_stride + (row_starts ? row_starts[b] : 0);
+  const int len = in.len(b);
+  const float* row = in.row(b);
 
   RowOut out;
   out.page = out_page + (int64_t)b * top_k;
@@ -180,37 +352,49 @@ topk_select_kernel(const float* __restrict__ scores, int64_t score_stride,
   for (int i = tid; i < nwords; i += kTopkThreads) s.bitmap[i] = 0u;
   for (int i = tid; i < kHistBins; i += kTopkThreads) s.hist[i] = 0u;
   if (tid < 2) s.list_count[tid] = 0u;
-  __syncthreads();
-
-  // Level-0 histogram: one coalesced pass over the row, 4 loads in flight per thread.
-  for (int base = 0; base < len; base += 4 * kTopkThreads) {
-    float x[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = base + j * kTopkThreads + tid;
-      x[j] = i < len ? row[i] : 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = base + j * kTopkThreads + tid;
-      if (i < len) atomicAdd(&s.hist[order_key(x[j]) >> 20], 1u);
-    }
-  }
+  const uint32_t cand = ws ? ws[b].count : 0u;
+  const bool listed = ws && cand >= (uint32_t)top_k && cand <= (uint32_t)kListCap;
   __syncthreads();
 
   uint32_t thr[kLevels] = {0, 0, 0, 0, 0};
   uint32_t remain = (uint32_t)top_k;
-  bool global_mode = true;
+  bool source_mode = !listed;  // level pass over the row (HBM) vs the LDS list
   int cur = 0;
   uint32_t list_n = 0;
 
+  if (listed) {
+    for (uint32_t e = tid; e < cand; e += kTopkThreads) {
+      const uint32_t key = ws[b].key[e];
+      s.list_key[0][e] = key;
+      s.list_pos[0][e] = ws[b].pos[e];
+      atomicAdd(&s.hist[key >> 20], 1u);
+    }
+    list_n = cand;
+  } else {
+    // Level-0 histogram: one coalesced pass over the row, 4 loads in flight per thread.
+    for (int base = 0; base < len; base += 4 * kTopkThreads) {
+      float x[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = base + j * kTopkThreads + tid;
+        x[j] = i < len ? row[i] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = base + j * kTopkThreads + tid;
+        if (i < len) atomicAdd(&s.hist[order_key(x[j]) >> 20], 1u);
+      }
+    }
+  }
+  __syncthreads();
+
   for (int level = 0; level < kLevels; ++level) {
-    find_threshold(s, radix_bins(level), remain);
+    find_threshold<kTopkThreads>(s.hist, s.wave_sum, radix_bins(level), remain, &s.tb, &s.above, &s.eq);
     const uint32_t tb = s.tb, above = s.above, eq = s.eq;
     thr[level] = tb;
     remain -= above;
     const bool take_all = (eq == remain) || level == kLevels - 1;
-    const bool collect = !take_all && (!global_mode || eq <= (uint32_t)kListCap);
+    const bool collect = !take_all && (!source_mode || eq <= (uint32_t)kListCap);
     const int nxt = cur ^ 1;
     __syncthreads();  // everyone has read tb/above/eq and the old histogram
     if (!take_all) {
@@ -219,7 +403,22 @@ topk_select_kernel(const float* __restrict__ scores, int64_t score_stride,
     }
     __syncthreads();
 
-    if (global_mode) {
+    // one element of the current bucket: mark, or pass on to the next digit
+    auto visit = [&](uint32_t key, uint32_t pos) {
+      const uint32_t d = radix_digit(level, key, pos);
+      if (d > tb || (take_all && d == tb)) atomicOr(&s.bitmap[pos >> 5], 1u << (pos & 31));
+      if (!take_all && d == tb) {
+        atomicAdd(&s.hist[radix_digit(level + 1, key, pos)], 1u);
+        if (collect) {
+          const uint32_t slot = atomicAdd(&s.list_count[nxt], 1u);
+          s.list_key[nxt][slot] = key;
+          s.list_pos[nxt][slot] = pos;
+        }
+      }
+    };
+
+    if (source_mode) {
+      // HBM pass over the row (the exact path with no bound)
       for (int base = 0; base < len; base += 4 * kTopkThreads) {
         float x[4];
 #pragma unroll
@@ -231,45 +430,16 @@ topk_select_kernel(const float* __restrict__ scores, int64_t score_stride,
         for (int j = 0; j < 4; ++j) {
           const int i = base + j * kTopkThreads + tid;
           const uint32_t key = order_key(x[j]);
-          bool sel = false;
-          if (i < len && in_bucket(level, key, (uint32_t)i, thr)) {
-            const uint32_t d = radix_digit(level, key, (uint32_t)i);
-            sel = d > tb || (take_all && d == tb);
-            if (!take_all && d == tb) {
-              atomicAdd(&s.hist[radix_digit(level + 1, key, (uint32_t)i)], 1u);
-              if (collect) {
-                const uint32_t slot = atomicAdd(&s.list_count[nxt], 1u);
-                s.list_key[nxt][slot] = key;
-                s.list_pos[nxt][slot] = (uint32_t)i;
-              }
-            }
-          }
-          // positions of one wave are 64 consecutive, 64-aligned -> two bitmap words
-          const uint64_t m = __ballot(sel);
-          if (lane == 0 && m) {
-            const int w0 = (base + j * kTopkThreads + wave * 64) >> 5;
-            if ((uint32_t)m) atomicOr(&s.bitmap[w0], (uint32_t)m);
-            if ((uint32_t)(m >> 32)) atomicOr(&s.bitmap[w0 + 1], (uint32_t)(m >> 32));
-          }
+          if (i < len && in_bucket(level, key, (uint32_t)i, thr)) visit(key, (uint32_t)i);
         }
       }
     } else {
-      for (uint32_t e = tid; e < list_n; e += kTopkThreads) {
-        const uint32_t key = s.list_key[cur][e], pos = s.list_pos[cur][e];
-        const uint32_t d = radix_digit(level, key, pos);
-        if (d > tb || (take_all && d == tb)) atomicOr(&s.bitmap[pos >> 5], 1u << (pos & 31));
-        if (!take_all && d == tb) {
-          atomicAdd(&s.hist[radix_digit(level + 1, key, pos)], 1u);
-          const uint32_t slot = atomicAdd(&s.list_count[nxt], 1u);
-          s.list_key[nxt][slot] = key;
-          s.list_pos[nxt][slot] = pos;
-        }
-      }
+      for (uint32_t e = tid; e < list_n; e += kTopkThreads) visit(s.list_key[cur][e], s.list_pos[cur][e]);
     }
     __syncthreads();
     if (take_all) break;
     if (collect) {
-      global_mode = false;
+      source_mode = false;
       cur = nxt;
       list_n = s.list_count[cur];
     }
@@ -281,17 +451,21 @@ topk_select_kernel(const float* __restrict__ scores, int64_t score_stride,
   uint32_t cnt = 0;
   for (int w = w_begin; w < w_end; ++w) cnt += __popc(s.bitmap[w]);
   uint32_t total = 0;
-  uint32_t slot = block_exclusive_scan(s, cnt, &total);
+  uint32_t slot = block_exclusive_scan<kTopkThreads>(s.wave_sum, cnt, &total);
+  // positions in ascending order into LDS, then the page-table translation as
+  // independent loads spread over all threads
+  uint32_t* sel = s.list_pos[0];
   for (int w = w_begin; w < w_end; ++w) {
     uint32_t bits = s.bitmap[w];
     while (bits) {
       const int bit = __ffs(bits) - 1;
       bits &= bits - 1;
-      if (slot < (uint32_t)top_k) out.emit((int)slot, (w << 5) + bit);
+      if (slot < (uint32_t)top_k) sel[slot] = (uint32_t)((w << 5) + bit);
       ++slot;
     }
   }
-  for (int i = (int)total + tid; i < top_k; i += kTopkThreads) out.emit(i, -1);
+  __syncthreads();
+  for (int i = tid; i < top_k; i += kTopkThreads) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
 }
 
 __global__ void topk_to_physical_kernel(const int32_t* __restrict__ topk, int64_t topk_stride,
@@ -316,7 +490,7 @@ __global__ void topk_to_physical_kernel(const int32_t* __restrict__ topk, int64_
 static int prepare_topk_kernel() {
   static int status = -1;
   if (status < 0) {
-    hipError_t e = hipFuncSetAttribute((const void*)topk_select_kernel,
+    hipError_t e = hipFuncSetAttribute((const void*)topk_finish_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTopkSmemBytes);
     status = e == hipSuccess ? 0 : 1;
     if (status) return set_error(kLaunchFailed, "topk: cannot reserve %zu B of LDS: %s",
@@ -325,16 +499,45 @@ static int prepare_topk_kernel() {
   return status ? kLaunchFailed : kOk;
 }
 
+// The launches of one selection. `workspace` NULL: the exact full path only.
+static int launch_topk(const RowIn& in, int batch, const int32_t* offsets, const int32_t* page_table,
+                       int64_t pt_stride, uint32_t page_bits, int32_t* out_page, int32_t* out_raw,
+                       int top_k, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                       const char* what) {
+  if (int rc = prepare_topk_kernel()) return rc;
+  RowWs* ws = nullptr;
+  if (workspace) {
+    if (workspace_bytes < (size_t)batch * sizeof(RowWs))
+      return set_error(kWorkspaceTooSmall, "%s: workspace %zu B < %zu B", what, workspace_bytes,
+                       (size_t)batch * sizeof(RowWs));
+    if (reinterpret_cast<uintptr_t>(workspace) & 15)
+      return set_error(kInvalidArgument, "%s: workspace must be 16-byte aligned", what);
+    ws = static_cast<RowWs*>(workspace);
+    hipLaunchKernelGGL(topk_threshold_kernel, dim3(batch), dim3(kAuxThreads), 0, stream, in, top_k, ws);
+    const int64_t spans = (in.max_len + kGatherSpan - 1) / kGatherSpan;
+    if (spans > 0)
+      hipLaunchKernelGGL(topk_gather_kernel, dim3((unsigned)spans, batch), dim3(kAuxThreads), 0, stream, in,
+                         top_k, ws);
+  }
+  hipLaunchKernelGGL(topk_finish_kernel, dim3(batch), dim3(kTopkThreads), kTopkSmemBytes, stream, in, ws,
+                     offsets, page_table, pt_stride, page_bits, out_page, out_raw, top_k);
+  return check_launch(what);
+}
+
 }  // namespace dsa
 
 extern "C" {
 
 int dsa_topk_max_len(void) { return dsa::kTopkMaxLen; }
 
+size_t dsa_topk_workspace_bytes(int batch) {
+  return batch > 0 ? (size_t)batch * sizeof(dsa::RowWs) : 0;
+}
+
 int dsa_topk_transform(const float* scores, int64_t score_stride, const int32_t* seq_lens,
                        const int32_t* page_table, int64_t page_table_stride, int32_t* out_page,
                        int32_t* out_raw, int batch, int64_t max_len, int page_size, int top_k,
-                       void* stream) {
+                       void* workspace, size_t workspace_bytes, void* stream) {
   using namespace dsa;
   if (top_k != 512 && top_k != 2048)
     return set_error(kInvalidArgument, "top_k must be 512 or 2048, got %d", top_k);
@@ -346,17 +549,17 @@ int dsa_topk_transform(const float* scores, int64_t score_stride, const int32_t*
     return set_error(kUnsupported, "score rows longer than %d are not supported (got %lld)",
                      kTopkMaxLen, (long long)max_len);
   if (batch == 0) return kOk;
-  if (int rc = prepare_topk_kernel()) return rc;
+  const RowIn in{scores, score_stride, seq_lens, nullptr, max_len};
   const uint32_t bits = (uint32_t)__builtin_ctz((unsigned)page_size);
-  hipLaunchKernelGGL(topk_select_kernel, dim3(batch), dim3(kTopkThreads), kTopkSmemBytes,
-                     (hipStream_t)stream, scores, score_stride, seq_lens, nullptr, nullptr, page_table,
-                     page_table_stride, bits, out_page, out_raw, max_len, top_k);
-  return check_launch("dsa_topk_transform");
+  return launch_topk(in, batch, nullptr, page_table, page_table_stride, bits, out_page,
+                     page_table ? out_raw : nullptr, top_k, workspace, workspace_bytes, (hipStream_t)stream,
+                     "dsa_topk_transform");
 }
 
 int dsa_topk_transform_ragged(const float* scores, int64_t score_stride, const int32_t* seq_lens,
                               const int32_t* row_starts, const int32_t* offsets, int32_t* out,
-                              int batch, int64_t max_len, int top_k, void* stream) {
+                              int batch, int64_t max_len, int top_k, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   using namespace dsa;
   if (top_k != 2048) return set_error(kInvalidArgument, "ragged Indexer top_k must be 2048, got %d", top_k);
   if (batch < 0 || max_len < 0 || (batch > 0 && (!scores || !seq_lens || !row_starts || !offsets || !out)))
@@ -365,11 +568,9 @@ int dsa_topk_transform_ragged(const float* scores, int64_t score_stride, const i
     return set_error(kUnsupported, "ragged rows longer than %d are not supported (got %lld)",
                      kTopkMaxLen, (long long)max_len);
   if (batch == 0) return kOk;
-  if (int rc = prepare_topk_kernel()) return rc;
-  hipLaunchKernelGGL(topk_select_kernel, dim3(batch), dim3(kTopkThreads), kTopkSmemBytes,
-                     (hipStream_t)stream, scores, score_stride, seq_lens, row_starts, offsets, nullptr,
-                     (int64_t)0, 0u, out, nullptr, max_len, top_k);
-  return check_launch("dsa_topk_transform_ragged");
+  const RowIn in{scores, score_stride, seq_lens, row_starts, max_len};
+  return launch_topk(in, batch, offsets, nullptr, 0, 0u, out, nullptr, top_k, workspace, workspace_bytes,
+                     (hipStream_t)stream, "dsa_topk_transform_ragged");
 }
 
 int dsa_topk_to_physical(const int32_t* topk_indices, int64_t topk_stride, const int32_t* block_table,

@@ -106,9 +106,35 @@ def indexer_logits(q_fp8: torch.Tensor, kv_cache: torch.Tensor, weights: torch.T
 
 
 # --------------------------------------------------------------------------- top-k
+_TOPK_WS: dict = {}
+
+
+def topk_workspace_bytes(batch: int) -> int:
+    return int(_lib.load().dsa_topk_workspace_bytes(batch))
+
+
+def topk_workspace(batch: int, device: torch.device) -> torch.Tensor:
+    """Workspace for the top-k entry points, cached per (device, stream) and
+    grown on demand; calls on one stream are ordered, so sharing is safe."""
+    need = int(_lib.load().dsa_topk_workspace_bytes(batch))
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _TOPK_WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+        _TOPK_WS[key] = ws
+    return ws
+
+
+def _ws_args(ws):
+    """(pointer, bytes) for a workspace tensor; False selects the path that
+    needs no workspace (the full multi-pass exact select)."""
+    return (None, 0) if ws is None or ws is False else (ws.data_ptr(), ws.numel())
+
+
 def topk_transform(scores: torch.Tensor, seq_lens: torch.Tensor, page_tables: torch.Tensor,
                    out_page_indices: torch.Tensor, page_size: int, top_k: int,
-                   out_raw_indices: torch.Tensor | None = None) -> None:
+                   out_raw_indices: torch.Tensor | None = None,
+                   workspace=None) -> None:
     if top_k not in (512, 2048):
         raise ValueError(f"top_k must be 512 or 2048, got {top_k}")
     _require(scores.dim() == 2 and scores.dtype == torch.float32 and scores.stride(1) == 1,
@@ -125,13 +151,16 @@ def topk_transform(scores: torch.Tensor, seq_lens: torch.Tensor, page_tables: to
     if page_size <= 0 or page_size & (page_size - 1):
         raise RuntimeError("page_size must be power of 2")
     dev = _check_cuda(scores, seq_lens, page_tables, out_page_indices)
+    if workspace is None:
+        workspace = topk_workspace(B, dev)
     _lib.call("dsa_topk_transform", scores.data_ptr(), scores.stride(0), seq_lens.data_ptr(),
               page_tables.data_ptr(), page_tables.stride(0), out_page_indices.data_ptr(),
-              _ptr(out_raw_indices), B, scores.shape[1], int(page_size), int(top_k), _stream(dev))
+              _ptr(out_raw_indices), B, scores.shape[1], int(page_size), int(top_k), *_ws_args(workspace),
+              _stream(dev))
 
 
 def topk_transform_raw(scores: torch.Tensor, seq_lens: torch.Tensor, out_indices: torch.Tensor,
-                       top_k: int) -> None:
+                       top_k: int, workspace=None) -> None:
     """Exact top-k positions without translation (``page_table`` NULL in the C ABI)."""
     if top_k not in (512, 2048):
         raise ValueError(f"top_k must be 512 or 2048, got {top_k}")
@@ -143,12 +172,16 @@ def topk_transform_raw(scores: torch.Tensor, seq_lens: torch.Tensor, out_indices
     _require(out_indices.dtype == torch.int32 and tuple(out_indices.shape) == (B, top_k)
              and out_indices.is_contiguous(), f"out_indices must be contiguous int32 [{B}, {top_k}]")
     dev = _check_cuda(scores, seq_lens, out_indices)
+    if workspace is None:
+        workspace = topk_workspace(B, dev)
     _lib.call("dsa_topk_transform", scores.data_ptr(), scores.stride(0), seq_lens.data_ptr(), None, 0,
-              out_indices.data_ptr(), None, B, scores.shape[1], 1, int(top_k), _stream(dev))
+              out_indices.data_ptr(), None, B, scores.shape[1], 1, int(top_k), *_ws_args(workspace),
+              _stream(dev))
 
 
 def topk_transform_ragged(scores: torch.Tensor, seq_lens: torch.Tensor, row_starts: torch.Tensor,
-                          offsets: torch.Tensor, out_indices: torch.Tensor, top_k: int) -> None:
+                          offsets: torch.Tensor, out_indices: torch.Tensor, top_k: int,
+                          workspace=None) -> None:
     if top_k != 2048:
         raise ValueError(f"ragged Indexer top_k must be 2048, got {top_k}")
     _require(scores.dim() == 2 and scores.dtype == torch.float32 and scores.stride(1) == 1,
@@ -160,9 +193,11 @@ def topk_transform_ragged(scores: torch.Tensor, seq_lens: torch.Tensor, row_star
     _require(out_indices.dtype == torch.int32 and tuple(out_indices.shape) == (B, top_k)
              and out_indices.is_contiguous(), "out_indices must be contiguous int32 [B, top_k]")
     dev = _check_cuda(scores, seq_lens, row_starts, offsets, out_indices)
+    if workspace is None:
+        workspace = topk_workspace(B, dev)
     _lib.call("dsa_topk_transform_ragged", scores.data_ptr(), scores.stride(0), seq_lens.data_ptr(),
               row_starts.data_ptr(), offsets.data_ptr(), out_indices.data_ptr(), B, scores.shape[1],
-              int(top_k), _stream(dev))
+              int(top_k), *_ws_args(workspace), _stream(dev))
 
 
 def topk_to_physical(topk_indices: torch.Tensor, block_table: torch.Tensor, block_size: int,

@@ -30,6 +30,7 @@ class DsaDecodeStep:
         self.num_splits = ops.sparse_mla_num_splits(rows, num_heads, index_topk, dev)
         need = ops.sparse_mla_workspace_bytes(rows, num_heads, self.num_splits)
         self.workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        self.topk_workspace = torch.empty(max(ops.topk_workspace_bytes(rows), 16), dtype=torch.uint8, device=dev)
 
     def expand_lens(self, context_lens: torch.Tensor) -> torch.Tensor:
         """Per-query causal lengths, flattened [batch*next_n] int32."""
@@ -51,7 +52,7 @@ class DsaDecodeStep:
         ops.indexer_logits(q_idx_fp8.view(B, n, *q_idx_fp8.shape[1:]), indexer_cache, weights,
                            seq_lens.view(B, n), block_tables, self.max_ctx, out=self.logits)
         ops.topk_transform(self.logits, seq_lens, page_tables, self.physical, self.page_size, self.topk,
-                           self.logical)
+                           self.logical, workspace=self.topk_workspace)
         ops.sparse_mla_decode(q_mla, kv_cache, self.physical, sm_scale, out=self.out, lse=self.lse,
                               num_splits=self.num_splits, workspace=self.workspace)
         return self.out, self.lse, self.logical, self.physical

@@ -16,12 +16,18 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(scores, lens, page_tables, page_size, top_k):
+    """Both selection routes (sampled candidate list, and the full multi-pass
+    select used without a workspace) must give the same exact answer."""
     B = scores.shape[0]
-    out = torch.empty(B, top_k, dtype=torch.int32, device=scores.device)
-    raw = torch.empty_like(out)
-    deepseek_v4.topk_transform(scores, lens, page_tables, out, page_size, top_k, raw)
-    torch.cuda.synchronize()
-    return out.cpu().numpy(), raw.cpu().numpy()
+    res = []
+    for ws in (None, False):
+        out = torch.full((B, top_k), 7, dtype=torch.int32, device=scores.device)
+        raw = torch.full_like(out, 7)
+        ops.topk_transform(scores, lens, page_tables, out, page_size, top_k, raw, workspace=ws)
+        torch.cuda.synchronize()
+        res.append((out.cpu().numpy(), raw.cpu().numpy()))
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1])
+    return res[0]
 
 
 @pytest.mark.parametrize("top_k", [512, 2048])
