@@ -56,16 +56,16 @@ __device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
   return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
 }
 
-// Dequantise 16 fp8 bytes (v4i) with a power-of-two scale into 16 bf16 (two v4i).
+// Dequantise 16 fp8 bytes (v4i) times `scale` into 16 bf16 (two v4i: dims
+// 0-7 and 8-15), one v_cvt_scalef32_pk_bf16_fp8 per pair of values. Exact for
+// power-of-two scales (an e4m3 value times 2^k is a bf16 value).
 __device__ __forceinline__ void dequant16_fp8_bf16(v4i raw, float scale, v4i& lo, v4i& hi) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    v2f a = fp8x2_to_f32((uint32_t)raw[w], false);
-    v2f b = fp8x2_to_f32((uint32_t)raw[w], true);
-    uint32_t p0 = pack_bf16_trunc(a.x * scale, a.y * scale);
-    uint32_t p1 = pack_bf16_trunc(b.x * scale, b.y * scale);
-    if (w < 2) { lo[2 * w] = (int)p0; lo[2 * w + 1] = (int)p1; }
-    else       { hi[2 * (w - 2)] = (int)p0; hi[2 * (w - 2) + 1] = (int)p1; }
+    const int p0 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[w], scale, false));
+    const int p1 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[w], scale, true));
+    if (w < 2) { lo[2 * w] = p0; lo[2 * w + 1] = p1; }
+    else       { hi[2 * (w - 2)] = p0; hi[2 * (w - 2) + 1] = p1; }
   }
 }
 

@@ -98,18 +98,25 @@ __device__ __forceinline__ void load_rows(RowRegs& rr, const MlaParams& P, int t
   }
 }
 
-__device__ __forceinline__ void stage_rows(const RowRegs& rr, uint8_t* buf, int lane, int wave) {
+// Stage piece i (0-7: a 16-dim nope chunk of the wave's tile; 8: the wave's
+// two rope chunks) of the lane's row into the bf16 tile.
+__device__ __forceinline__ void stage_piece(const RowRegs& rr, uint8_t* buf, int lane, int wave, int i) {
   uint8_t* krow = buf + lane * kPitch;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int c = wave * 8 + i;  // 16-dim chunk index, dims 16c .. 16c+15
+  if (i < 8) {
+    const int c = wave * 8 + i;  // dims 16c .. 16c+15
     v4i lo, hi;
     dequant16_fp8_bf16(rr.nope[i], rr.scale, lo, hi);
     *reinterpret_cast<v4i*>(krow + c * 32) = lo;
     *reinterpret_cast<v4i*>(krow + c * 32 + 16) = hi;
+  } else {
+    *reinterpret_cast<v4i*>(krow + 1024 + wave * 32) = rr.rope[0];
+    *reinterpret_cast<v4i*>(krow + 1024 + wave * 32 + 16) = rr.rope[1];
   }
-  *reinterpret_cast<v4i*>(krow + 1024 + wave * 32) = rr.rope[0];
-  *reinterpret_cast<v4i*>(krow + 1024 + wave * 32 + 16) = rr.rope[1];
+}
+
+__device__ __forceinline__ void stage_rows(const RowRegs& rr, uint8_t* buf, int lane, int wave) {
+#pragma unroll
+  for (int i = 0; i < 9; ++i) stage_piece(rr, buf, lane, wave, i);
 }
 
 __device__ __forceinline__ v8bf as_v8bf(v4i x) { return __builtin_bit_cast(v8bf, x); }
@@ -172,20 +179,31 @@ sparse_mla_kernel(const MlaParams P) {
 
   for (int n = 0; n < nblk; ++n) {
     const uint8_t* buf = smem + (n & 1) * kBufBytes;
+    uint8_t* next_buf = smem + ((n + 1) & 1) * kBufBytes;
+    const bool stage_next = n + 1 < nblk;
+    const uint64_t vm_next = stage_next ? __ballot(rr.valid) : 0ull;
     if (active && vm_cur) {
-      // ---- S^T = K . Q^T: s[kt][r] = score(key kt*16 + 4g + r, head c16)
+      // ---- S^T = K . Q^T: s[kt][r] = score(key kt*16 + 4g + r, head c16).
+      // A operands are read two k-steps ahead of their MFMAs.
       v4f s[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) s[kt] = (v4f){0.f, 0.f, 0.f, 0.f};
       const uint8_t* arow = buf + c16 * kPitch + g * 16;
+      v4i a[3][4];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) a[ks][kt] = *reinterpret_cast<const v4i*>(arow + kt * 16 * kPitch + ks * 64);
 #pragma unroll
       for (int ks = 0; ks < 18; ++ks) {
-        v4i a[4];
+        if (ks + 2 < 18) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) a[kt] = *reinterpret_cast<const v4i*>(arow + kt * 16 * kPitch + ks * 64);
+          for (int kt = 0; kt < 4; ++kt)
+            a[(ks + 2) % 3][kt] = *reinterpret_cast<const v4i*>(arow + kt * 16 * kPitch + (ks + 2) * 64);
+        }
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
-          s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a[kt]), as_v8bf(qb[ks]), s[kt], 0, 0, 0);
+          s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a[ks % 3][kt]), as_v8bf(qb[ks]), s[kt], 0, 0, 0);
       }
 
       // ---- online softmax (exp2 domain), lazy rescale
@@ -225,30 +243,40 @@ sparse_mla_kernel(const MlaParams P) {
         }
       l_run += psum;
 
-      // ---- O += P . V
+      // ---- O += P . V, V operands two tiles ahead; the next block's rows are
+      // dequantised into the other buffer between the MFMAs.
+      v4i pa[2];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        v4i pa;
-        pa[0] = cvt_pk_bf16(s[2 * kk][0], s[2 * kk][1]);
-        pa[1] = cvt_pk_bf16(s[2 * kk][2], s[2 * kk][3]);
-        pa[2] = cvt_pk_bf16(s[2 * kk + 1][0], s[2 * kk + 1][1]);
-        pa[3] = cvt_pk_bf16(s[2 * kk + 1][2], s[2 * kk + 1][3]);
-        // lane (g, c16) addresses key row 32kk + 4g + c16/4 (and +16), dv 4*(c16%4) of each 16-dv tile
-        const uint8_t* v1 = buf + (32 * kk + 4 * g + (c16 >> 2)) * kPitch + (c16 & 3) * 8;
-        const uint8_t* v2 = v1 + 16 * kPitch;
-#pragma unroll
-        for (int dt = 0; dt < 32; ++dt) {
-          const v4s b1 = lds_read_tr16(v1 + dt * 32);
-          const v4s b2 = lds_read_tr16(v2 + dt * 32);
-          const v8bf b = __builtin_bit_cast(v8bf, __builtin_shufflevector(b1, b2, 0, 1, 2, 3, 4, 5, 6, 7));
-          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(pa), b, o[dt], 0, 0, 0);
-        }
+        pa[kk][0] = cvt_pk_bf16(s[2 * kk][0], s[2 * kk][1]);
+        pa[kk][1] = cvt_pk_bf16(s[2 * kk][2], s[2 * kk][3]);
+        pa[kk][2] = cvt_pk_bf16(s[2 * kk + 1][0], s[2 * kk + 1][1]);
+        pa[kk][3] = cvt_pk_bf16(s[2 * kk + 1][2], s[2 * kk + 1][3]);
       }
-    }
-    uint64_t vm_next = 0;
-    if (n + 1 < nblk) {
-      vm_next = __ballot(rr.valid);
-      stage_rows(rr, smem + ((n + 1) & 1) * kBufBytes, lane, wave);
+      // lane (g, c16) addresses key row 4g + c16/4 (+16, +32, +48), dv 4*(c16%4) of each 16-dv tile
+      const uint8_t* vb = buf + (4 * g + (c16 >> 2)) * kPitch + (c16 & 3) * 8;
+      v4s vv[3][4];
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) vv[dt][q] = lds_read_tr16(vb + q * 16 * kPitch + dt * 32);
+#pragma unroll
+      for (int dt = 0; dt < 32; ++dt) {
+        if (dt + 2 < 32) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) vv[(dt + 2) % 3][q] = lds_read_tr16(vb + q * 16 * kPitch + (dt + 2) * 32);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const v8bf bop = __builtin_bit_cast(
+              v8bf, __builtin_shufflevector(vv[dt % 3][2 * kk], vv[dt % 3][2 * kk + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(pa[kk]), bop, o[dt], 0, 0, 0);
+        }
+        if (stage_next && (dt & 3) == 3) stage_piece(rr, next_buf, lane, wave, dt >> 2);
+      }
+      if (stage_next) stage_piece(rr, next_buf, lane, wave, 8);
+    } else if (stage_next) {
+      stage_rows(rr, next_buf, lane, wave);
     }
     if (n + 2 < nblk) load_rows(rr, P, t, key_begin + (n + 2) * kMlaKeys, lane, wave);
     __syncthreads();
