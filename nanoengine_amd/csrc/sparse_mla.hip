@@ -8,10 +8,12 @@
 // Workgroup = 4 waves = 64 heads of one token over one key split; each wave
 // owns 16 heads. Per block of 64 selected rows:
 //   load   : lane = row; wave w gathers tile w of the 64 rows (8 x 16 B fp8 +
-//            its f32 scale) and two 16 B rope chunks, two blocks ahead of use;
-//   stage  : rows are dequantised in registers (fp8 * 2^k is exact in bf16)
-//            and written once, row-major, into one of two LDS buffers
-//            [64][576] bf16 (double buffering: one barrier per block);
+//            its f32 scale) and two 16 B rope chunks, a full block of compute
+//            ahead of use (the row indices one block further ahead);
+//   stage  : rows are dequantised in registers (fp8 * 2^k is exact in bf16,
+//            one v_cvt_scalef32_pk_bf16_fp8 per pair) and written once,
+//            row-major, into one of two LDS buffers [64][576] bf16 (double
+//            buffering: one barrier per block), between the QK MFMAs;
 //   QK     : S^T[64 keys x 16 heads] on v_mfma_f32_16x16x32_bf16, A = rows
 //            from LDS (four independent accumulator chains), B = the wave's
 //            16 query heads, resident in registers for the whole kernel;
@@ -74,9 +76,12 @@ struct RowRegs {
   bool valid;
 };
 
-__device__ __forceinline__ void load_rows(RowRegs& rr, const MlaParams& P, int t, int key0, int lane,
-                                          int wave) {
-  const int32_t slot = P.idx[(int64_t)t * P.idx_stride + key0 + lane];
+__device__ __forceinline__ int32_t load_slot(const MlaParams& P, int t, int key0, int lane) {
+  return P.idx[(int64_t)t * P.idx_stride + key0 + lane];
+}
+
+// Gather this wave's share of the lane's row (`slot` < 0: an invalid index, zeros).
+__device__ __forceinline__ void load_rows(RowRegs& rr, const MlaParams& P, int32_t slot, int wave) {
   rr.valid = slot >= 0;
   if (rr.valid) {
     const uint8_t* row = P.kv + (int64_t)(slot / P.kv_block_size) * P.kv_blk_stride +
@@ -170,11 +175,16 @@ sparse_mla_kernel(const MlaParams P) {
   float m_run = -__builtin_inff();  // per head c16, log2 domain
   float l_run = 0.f;                // per head c16, this lane's keys only
 
+  // Pipeline: block n is multiplied from LDS while block n+1 (in registers)
+  // is staged into the other buffer and block n+2's rows are in flight; the
+  // row indices run one block further ahead.
   RowRegs rr;
-  load_rows(rr, P, t, key_begin, lane, wave);
+  load_rows(rr, P, load_slot(P, t, key_begin, lane), wave);
+  int32_t slot_pf = nblk > 1 ? load_slot(P, t, key_begin + kMlaKeys, lane) : -1;
   uint64_t vm_cur = __ballot(rr.valid);
   stage_rows(rr, smem, lane, wave);
-  if (nblk > 1) load_rows(rr, P, t, key_begin + kMlaKeys, lane, wave);
+  if (nblk > 1) load_rows(rr, P, slot_pf, wave);
+  if (nblk > 2) slot_pf = load_slot(P, t, key_begin + 2 * kMlaKeys, lane);
   __syncthreads();
 
   for (int n = 0; n < nblk; ++n) {
@@ -204,6 +214,13 @@ sparse_mla_kernel(const MlaParams P) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
           s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a[ks % 3][kt]), as_v8bf(qb[ks]), s[kt], 0, 0, 0);
+        if (stage_next && (ks & 1)) stage_piece(rr, next_buf, lane, wave, ks >> 1);
+      }
+      // block n+1 is staged: its registers take block n+2's rows now, which
+      // leaves them a whole block of compute to arrive
+      if (n + 2 < nblk) {
+        load_rows(rr, P, slot_pf, wave);
+        if (n + 3 < nblk) slot_pf = load_slot(P, t, key_begin + (n + 3) * kMlaKeys, lane);
       }
 
       // ---- online softmax (exp2 domain), lazy rescale
@@ -243,8 +260,7 @@ sparse_mla_kernel(const MlaParams P) {
         }
       l_run += psum;
 
-      // ---- O += P . V, V operands two tiles ahead; the next block's rows are
-      // dequantised into the other buffer between the MFMAs.
+      // ---- O += P . V, V operands two tiles ahead
       v4i pa[2];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
@@ -272,13 +288,14 @@ sparse_mla_kernel(const MlaParams P) {
               v8bf, __builtin_shufflevector(vv[dt % 3][2 * kk], vv[dt % 3][2 * kk + 1], 0, 1, 2, 3, 4, 5, 6, 7));
           o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(pa[kk]), bop, o[dt], 0, 0, 0);
         }
-        if (stage_next && (dt & 3) == 3) stage_piece(rr, next_buf, lane, wave, dt >> 2);
       }
-      if (stage_next) stage_piece(rr, next_buf, lane, wave, 8);
-    } else if (stage_next) {
-      stage_rows(rr, next_buf, lane, wave);
+    } else {
+      if (stage_next) stage_rows(rr, next_buf, lane, wave);
+      if (n + 2 < nblk) {
+        load_rows(rr, P, slot_pf, wave);
+        if (n + 3 < nblk) slot_pf = load_slot(P, t, key_begin + (n + 3) * kMlaKeys, lane);
+      }
     }
-    if (n + 2 < nblk) load_rows(rr, P, t, key_begin + (n + 2) * kMlaKeys, lane, wave);
     __syncthreads();
     vm_cur = vm_next;
   }

@@ -1,0 +1,83 @@
+"""CPU checks of the C ABI: the library builds and loads, exports exactly the
+symbols include/dsa_amd.h declares, and rejects bad arguments with the
+documented status codes before touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsa_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"DSA_API\s+[\w\s\*]+?\b(dsa_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from nanoengine_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        from nanoengine_amd import build
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_reference_replacements():
+    names = _declared()
+    for n in ["dsa_indexer_logits", "dsa_indexer_schedule", "dsa_num_cus", "dsa_topk_transform",
+              "dsa_topk_transform_ragged", "dsa_topk_to_physical", "dsa_sparse_mla_decode"]:
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    from nanoengine_amd import _lib
+    for name in _declared():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(_declared())
+
+
+def test_version_and_error_string(lib):
+    assert lib.dsa_version() >= 100
+    assert lib.dsa_topk_max_len() == 1 << 18
+
+
+def test_argument_errors_return_status_without_a_device(lib):
+    from nanoengine_amd import _lib
+    P = None
+    # top_k outside {512, 2048} -> invalid argument (1)
+    rc = lib.dsa_topk_transform(P, 0, P, P, 0, P, P, 1, 10, 64, 1000, P, 0, P)
+    assert rc == 1 and b"512 or 2048" in lib.dsa_last_error()
+    # page size not a power of two
+    assert lib.dsa_topk_transform(P, 0, P, P, 0, P, P, 1, 10, 48, 512, P, 0, P) == 1
+    assert b"power of 2" in lib.dsa_last_error()
+    # ragged top_k must be 2048
+    assert lib.dsa_topk_transform_ragged(P, 0, P, P, P, P, 1, 10, 512, P, 0, P) == 1
+    # rows longer than the bitmap -> unsupported (2)
+    assert lib.dsa_topk_transform(P, 0, P, P, 0, P, P, 1, (1 << 18) + 1, 64, 2048, P, 0, P) in (1, 2)
+    # indexer shape limits
+    assert lib.dsa_indexer_logits(P, P, P, P, P, 0, 1, 1, 32, 128, 64, 64, P, 64, P) == 2
+    assert lib.dsa_indexer_logits(P, P, P, P, P, 0, 1, 3, 64, 128, 64, 64, P, 64, P) == 2
+    # sparse MLA: heads must be a multiple of 16, topk a multiple of 64
+    assert lib.dsa_sparse_mla_decode(P, 0, 0, P, 42640, 64, P, 0, 1, 24, 2048, ctypes.c_float(0.1), P, P, 1,
+                                     P, 0, P) == 2
+    assert lib.dsa_sparse_mla_decode(P, 0, 0, P, 42640, 64, P, 0, 1, 128, 100, ctypes.c_float(0.1), P, P, 1,
+                                     P, 0, P) == 2
+    # empty batches are a no-op success
+    assert lib.dsa_topk_transform(P, 0, P, P, 0, P, P, 0, 0, 64, 2048, P, 0, P) == 0
+    with pytest.raises(ValueError):
+        _lib.check(1, "probe")
+
+
+def test_workspace_size_queries(lib):
+    assert lib.dsa_topk_workspace_bytes(0) == 0
+    assert lib.dsa_topk_workspace_bytes(128) == 128 * (16 + 8 * 4096)
+    assert lib.dsa_sparse_mla_workspace_bytes(128, 128, 1) == 0
+    assert lib.dsa_sparse_mla_workspace_bytes(32, 128, 4) == 4 * 32 * 128 * (512 + 1) * 4
+    # splits grow until the grid covers the CUs, in 64-row blocks of top-k
+    assert lib.dsa_sparse_mla_num_splits(128, 128, 2048, 256) == 1
+    assert lib.dsa_sparse_mla_num_splits(32, 128, 2048, 256) == 4
+    assert lib.dsa_sparse_mla_num_splits(1, 16, 128, 256) == 2

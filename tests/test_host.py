@@ -1,0 +1,66 @@
+"""Host-side logic of the reference-mirroring Python layer (CPU only)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from nanoengine_amd import indexer, ops
+
+
+def test_expand_decode_context_lens_mirrors_reference():
+    # tests/test_shared_indexer.py:162-181
+    got = indexer._expand_decode_context_lens(torch.tensor([4098, 513], dtype=torch.int64), 2)
+    assert got.dtype == torch.int32 and got.tolist() == [[4097, 4098], [512, 513]]
+    assert indexer._expand_decode_context_lens(torch.tensor([1], dtype=torch.int32), 8).tolist() == [[1] * 8]
+    with pytest.raises(ValueError, match="batch"):
+        indexer._expand_decode_context_lens(torch.zeros(2, 3), 2)
+    for n in (1, 2, 3):
+        c = torch.randint(1, 5000, (7,))
+        assert np.array_equal(indexer._expand_decode_context_lens(c, n).numpy(),
+                              O.expand_decode_context_lens(c.numpy(), n))
+
+
+def test_linear_mtp_path_rule():
+    # tests/test_shared_indexer.py:184-187
+    assert not indexer._uses_linear_mtp_indexer_path(is_prefill=True, ntps=22)
+    assert not indexer._uses_linear_mtp_indexer_path(is_prefill=False, ntps=2)
+    assert indexer._uses_linear_mtp_indexer_path(is_prefill=False, ntps=3)
+
+
+def test_indexer_cache_layout_checks():
+    c = indexer.IndexerCache(num_layers=2, num_pages=16, page_size=64, head_dim=128, device="cpu")
+    assert c.bytes_per_token == 132 and c.get_buffer(1).shape == (16, 64 * 132)
+    with pytest.raises(ValueError, match="uint8"):
+        indexer.IndexerCache(1, 4, 64, 128, device="cpu", buffer=torch.zeros(1, 4, 10, dtype=torch.uint8))
+
+
+def test_ops_reject_host_tensors_and_bad_shapes():
+    s = torch.zeros(2, 128)
+    lens = torch.zeros(2, dtype=torch.int32)
+    out = torch.zeros(2, 512, dtype=torch.int32)
+    with pytest.raises(ValueError, match="512 or 2048"):
+        ops.topk_transform(s, lens, torch.zeros(2, 2, dtype=torch.int32), out, 64, 100)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops.topk_transform(s, lens, torch.zeros(2, 2, dtype=torch.int32), out, 64, 512)
+    with pytest.raises(RuntimeError, match="seq_lens"):
+        ops.topk_transform(s, lens.long(), torch.zeros(2, 2, dtype=torch.int32), out, 64, 512)
+    with pytest.raises(RuntimeError, match="656"):
+        ops.mla_kv_geometry(torch.zeros(4, 64, 1, 576, dtype=torch.uint8))
+    kv = torch.zeros(4, 65, 1, 656, dtype=torch.uint8)[:, :64]
+    assert ops.mla_kv_geometry(kv) == (65 * 656, 64)
+
+
+def test_golden_fixture_reproduces_from_the_oracle():
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "config0_indexer.npz"))
+    logits = O.indexer_logits(g["q_fp8"], g["cache"], g["weights"], g["context_lens"], g["block_tables"],
+                              g["logits"].shape[1])
+    np.testing.assert_array_equal(np.isfinite(logits), np.isfinite(g["logits"]))
+    np.testing.assert_allclose(logits[np.isfinite(logits)], g["logits"][np.isfinite(g["logits"])], rtol=1e-6)
+    page, raw = O.topk_transform(g["logits"], g["context_lens"].reshape(-1), g["block_tables"], 64, 2048)
+    assert np.array_equal(raw, g["topk_raw"]) and np.array_equal(page, g["topk_page"])
+    # the selected set agrees with torch.topk on every row
+    for b, L in enumerate(g["context_lens"].reshape(-1)):
+        k = min(int(L), 2048)
+        ref = torch.topk(torch.from_numpy(g["logits"][b, :L]), k).indices.numpy()
+        assert set(ref.tolist()) == set(raw[b, :k].tolist())
