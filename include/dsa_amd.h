@@ -170,6 +170,32 @@ DSA_API int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t
                           void* out, float* lse, int num_splits,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Quantise and store MLA KV rows into the packed fp8 cache.
+ *   kv          [num_tokens, 576] bf16 (row stride kv_row_stride elements, 16-byte aligned rows)
+ *   slots       [num_tokens] physical slots (int32, or int64 when slot_is_64), < 0 skipped
+ *   kv_cache    block b row r at kv_cache + b*kv_block_stride_bytes + r*656
+ * Row: e4m3fn(nope / s_t) for the four 128-dim tiles, s_t = 2^ceil(log2(max(amax_t/448,
+ * 1e-12))) as f32, then the 64 rope values as bf16.
+ * Replaces store_kcache_fp8(k, k_cache, slot_mapping)
+ * (dlengine/runtime/kernel/triton/hopper/fp8_utils.py:202-305, called at
+ *  dlengine/runtime/layers/backends/mla/flash_mla.py:42). */
+DSA_API int dsa_mla_kv_store(const void* kv, int64_t kv_row_stride, const void* slots,
+                             int slot_is_64, int num_tokens, uint8_t* kv_cache,
+                             int64_t kv_block_stride_bytes, int kv_block_size, void* stream);
+
+/* Quantise and store indexer keys into the split page layout.
+ *   k           [num_tokens, 128] bf16 (row stride k_row_stride elements)
+ *   slots       [num_tokens] flat slots (int32, or int64 when slot_is_64), < 0 skipped
+ *   cache       [pages, page_size*132] bytes
+ * code = e4m3fn(x / sf), sf = 2^ceil(log2(max(amax, 1e-4) / 448)); fp8 at
+ * page*page_size*132 + off*128, f32 scale at page*page_size*132 + page_size*128 + off*4.
+ * Replaces IndexerCache.store_key_fp8 / store_indexer_key_fp8_fused
+ * (dlengine/runtime/layers/backends/dsa/indexer/lightning.py:449-535,
+ *  dlengine/runtime/kernel/triton/generic/fp8_ue8m0_quant.py:369-440). */
+DSA_API int dsa_indexer_k_store(const void* k, int64_t k_row_stride, const void* slots,
+                                int slot_is_64, int num_tokens, uint8_t* cache, int page_size,
+                                void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

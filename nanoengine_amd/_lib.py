@@ -31,6 +31,8 @@ SIGNATURES = {
     "dsa_sparse_mla_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "dsa_sparse_mla_decode": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int, _P, c_int64, c_int, c_int,
                                       c_int, c_float, _P, _P, c_int, _P, c_size_t, _P]),
+    "dsa_mla_kv_store": (c_int, [_P, c_int64, _P, c_int, c_int, _P, c_int64, c_int, _P]),
+    "dsa_indexer_k_store": (c_int, [_P, c_int64, _P, c_int, c_int, _P, c_int, _P]),
 }
 
 _lib = None

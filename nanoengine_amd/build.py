@@ -13,7 +13,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libdsa_amd.so"
-SOURCES = ["capi.hip", "topk.hip", "indexer.hip", "sparse_mla.hip"]
+SOURCES = ["capi.hip", "topk.hip", "indexer.hip", "sparse_mla.hip", "cache_store.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

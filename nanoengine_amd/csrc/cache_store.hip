@@ -1,0 +1,133 @@
+// fp8 cache writers for the DSA path, for gfx950: the 656-byte MLA row and the
+// 132-byte indexer key (split page layout). One wave per token.
+//
+// MLA row (dlengine/runtime/kernel/triton/hopper/fp8_utils.py:32-108):
+//   bytes [0,512)   e4m3fn(nope / s_t), four 128-dim tiles t
+//   bytes [512,528) s_t = 2^ceil(log2(max(amax_t / 448, 1e-12))) as f32
+//   bytes [528,656) the 64 rope values, bf16, unchanged
+// Indexer key (dlengine/runtime/layers/backends/dsa/indexer/lightning.py:78-101,
+// page layout :494-507): page = [page_size x 128 fp8][page_size x f32 scale],
+//   sf = 2^ceil(log2(max(amax, 1e-4) / 448)), code = e4m3fn(x * (1/sf)).
+// Slots < 0 are skipped (the reference writes them harmlessly or not at all).
+#include "dsa_common.h"
+#include "../../include/dsa_amd.h"
+
+namespace dsa {
+
+// 2^ceil(log2(v)) for finite v > 0, exactly: v = 2^e * 1.m, ceil is e when the
+// mantissa is zero and e + 1 otherwise.
+__device__ __forceinline__ float pow2_ceil(float v) {
+  const uint32_t u = __float_as_uint(v);
+  int e = (int)((u >> 23) & 0xff);
+  const uint32_t m = u & 0x7fffffu;
+  if (e == 0) {  // subnormal: v = m * 2^-149
+    const int msb = 31 - __clz(m);
+    const int k = msb - 149 + ((m & (m - 1)) ? 1 : 0);
+    return ldexpf(1.f, k);
+  }
+  const int k = e - 127 + (m ? 1 : 0);
+  return ldexpf(1.f, k);
+}
+
+// Four floats -> four e4m3fn bytes (round to nearest even).
+__device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+__device__ __forceinline__ int64_t load_slot(const void* slots, int slot_is_64, int i) {
+  return slot_is_64 ? reinterpret_cast<const int64_t*>(slots)[i] : (int64_t)reinterpret_cast<const int32_t*>(slots)[i];
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__global__ void __launch_bounds__(256)
+mla_kv_store_kernel(const uint16_t* __restrict__ kv, int64_t row_stride, const void* __restrict__ slots,
+                    int slot_is_64, int n, uint8_t* __restrict__ cache, int64_t block_stride, int block_size) {
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= n) return;
+  const int64_t slot = load_slot(slots, slot_is_64, tok);
+  if (slot < 0) return;
+  const uint16_t* src = kv + (int64_t)tok * row_stride;
+  uint8_t* row = cache + (slot / block_size) * block_stride + (slot % block_size) * 656;
+  // nope: lane l holds dims 8l .. 8l+7 (tile l/16)
+  const v4i raw = *reinterpret_cast<const v4i*>(src + 8 * lane);
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = bf16_to_f32((uint16_t)raw[i]);
+    x[2 * i + 1] = bf16_to_f32((uint16_t)((uint32_t)raw[i] >> 16));
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, shfl_xor(amax, off));
+  const float s = pow2_ceil(fmaxf(amax / 448.f, 1e-12f));
+  uint2 codes;
+  codes.x = f32x4_to_fp8(x[0] / s, x[1] / s, x[2] / s, x[3] / s);
+  codes.y = f32x4_to_fp8(x[4] / s, x[5] / s, x[6] / s, x[7] / s);
+  *reinterpret_cast<uint2*>(row + 8 * lane) = codes;
+  if ((lane & 15) == 0) reinterpret_cast<float*>(row + 512)[lane >> 4] = s;
+  // rope: lanes 0-15 copy 4 bf16 each
+  if (lane < 16) *reinterpret_cast<uint2*>(row + 528 + 8 * lane) = *reinterpret_cast<const uint2*>(src + 512 + 4 * lane);
+}
+
+__global__ void __launch_bounds__(256)
+indexer_k_store_kernel(const uint16_t* __restrict__ k, int64_t row_stride, const void* __restrict__ slots,
+                       int slot_is_64, int n, uint8_t* __restrict__ cache, int page_size) {
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= n) return;
+  const int64_t slot = load_slot(slots, slot_is_64, tok);
+  if (slot < 0) return;
+  const uint32_t two = *reinterpret_cast<const uint32_t*>(k + (int64_t)tok * row_stride + 2 * lane);
+  const float a = bf16_to_f32((uint16_t)two), b = bf16_to_f32((uint16_t)(two >> 16));
+  float amax = fmaxf(fabsf(a), fabsf(b));
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, shfl_xor(amax, off));
+  const float sf = pow2_ceil(fmaxf(amax, 1e-4f) / 448.f);
+  const float inv = 1.f / sf;
+  const int64_t page = slot / page_size, off = slot % page_size;
+  uint8_t* base = cache + page * (int64_t)page_size * 132;
+  const uint32_t w = f32x4_to_fp8(a * inv, b * inv, 0.f, 0.f);
+  *reinterpret_cast<uint16_t*>(base + off * 128 + 2 * lane) = (uint16_t)w;
+  if (lane == 0) reinterpret_cast<float*>(base + (int64_t)page_size * 128)[off] = sf;
+}
+
+}  // namespace dsa
+
+extern "C" {
+
+int dsa_mla_kv_store(const void* kv, int64_t kv_row_stride, const void* slots, int slot_is_64, int num_tokens,
+                     uint8_t* kv_cache, int64_t kv_block_stride_bytes, int kv_block_size, void* stream) {
+  using namespace dsa;
+  if (num_tokens < 0 || kv_block_size <= 0 || kv_block_stride_bytes < (int64_t)kv_block_size * 656)
+    return set_error(kInvalidArgument, "dsa_mla_kv_store: bad sizes");
+  if (num_tokens == 0) return kOk;
+  if (!kv || !slots || !kv_cache) return set_error(kInvalidArgument, "dsa_mla_kv_store: null pointer");
+  if ((reinterpret_cast<uintptr_t>(kv) & 15) || (kv_row_stride % 8) || (kv_block_stride_bytes % 8) ||
+      (reinterpret_cast<uintptr_t>(kv_cache) & 7))
+    return set_error(kInvalidArgument, "dsa_mla_kv_store: kv rows must be 16-byte aligned, cache 8-byte aligned");
+  hipLaunchKernelGGL(mla_kv_store_kernel, dim3((num_tokens + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const uint16_t*>(kv), kv_row_stride, slots, slot_is_64, num_tokens, kv_cache,
+                     kv_block_stride_bytes, kv_block_size);
+  return check_launch("dsa_mla_kv_store");
+}
+
+int dsa_indexer_k_store(const void* k, int64_t k_row_stride, const void* slots, int slot_is_64, int num_tokens,
+                        uint8_t* cache, int page_size, void* stream) {
+  using namespace dsa;
+  if (num_tokens < 0 || page_size <= 0) return set_error(kInvalidArgument, "dsa_indexer_k_store: bad sizes");
+  if (num_tokens == 0) return kOk;
+  if (!k || !slots || !cache) return set_error(kInvalidArgument, "dsa_indexer_k_store: null pointer");
+  if ((reinterpret_cast<uintptr_t>(k) & 3) || (k_row_stride % 2))
+    return set_error(kInvalidArgument, "dsa_indexer_k_store: key rows must be 4-byte aligned");
+  hipLaunchKernelGGL(indexer_k_store_kernel, dim3((num_tokens + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const uint16_t*>(k), k_row_stride, slots, slot_is_64, num_tokens, cache, page_size);
+  return check_launch("dsa_indexer_k_store");
+}
+
+}  // extern "C"

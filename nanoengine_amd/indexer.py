@@ -64,6 +64,11 @@ class IndexerCache:
     def get_buffer(self, layer_id: int) -> torch.Tensor:
         return self.buffer[layer_id]
 
+    def store_key_fp8(self, layer_id: int, key_bf16: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+        """Quantise keys [N, head_dim] bf16 (UE8M0 per-token scale) and write them
+        into the split page layout (lightning.py:449-535), on the GPU."""
+        ops.indexer_k_store(key_bf16, self.buffer[layer_id], slot_mapping, self.page_size)
+
 
 def indexer_decode_topk(q_fp8: torch.Tensor, weights: torch.Tensor, kv_cache_buf: torch.Tensor,
                         context_lens: torch.Tensor, block_tables: torch.Tensor, index_topk: int,

@@ -275,3 +275,35 @@ def sparse_mla_decode(q: torch.Tensor, k_cache: torch.Tensor, indices: torch.Ten
               blk_stride, block_size, indices.data_ptr(), indices.stride(0), T, H, topk, float(sm_scale),
               out.data_ptr(), lse.data_ptr(), int(num_splits), ws_ptr, ws_bytes, _stream(dev))
     return out, lse
+
+
+# --------------------------------------------------------------------------- cache writers
+def _slots(slot_mapping: torch.Tensor, n: int) -> tuple[torch.Tensor, int]:
+    _require(slot_mapping.dim() == 1 and slot_mapping.shape[0] >= n, "slot_mapping must be 1-D with >= n entries")
+    _require(slot_mapping.dtype in (torch.int32, torch.int64), f"slot_mapping dtype {slot_mapping.dtype}")
+    s = slot_mapping.contiguous()
+    return s, int(s.dtype == torch.int64)
+
+
+def mla_kv_store(kv: torch.Tensor, k_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Quantise kv [N, (1,) 576] bf16 into the fp8 MLA cache at slot_mapping (see dsa_mla_kv_store)."""
+    kv2 = kv.reshape(kv.shape[0], -1)
+    _require(kv2.shape[1] == MLA_D_QK and kv2.dtype == torch.bfloat16 and kv2.stride(1) == 1,
+             f"kv must be bf16 [N, {MLA_D_QK}] with a contiguous last dim")
+    blk_stride, block_size = mla_kv_geometry(k_cache)
+    slots, is64 = _slots(slot_mapping, kv2.shape[0])
+    dev = _check_cuda(kv2, k_cache, slots)
+    _lib.call("dsa_mla_kv_store", kv2.data_ptr(), kv2.stride(0), slots.data_ptr(), is64, kv2.shape[0],
+              _as_bytes(k_cache).data_ptr(), blk_stride, block_size, _stream(dev))
+
+
+def indexer_k_store(key: torch.Tensor, cache: torch.Tensor, slot_mapping: torch.Tensor, page_size: int) -> None:
+    """Quantise indexer keys [N, 128] bf16 into the split page layout (see dsa_indexer_k_store)."""
+    _require(key.dim() == 2 and key.shape[1] == INDEXER_HEAD_DIM and key.dtype == torch.bfloat16
+             and key.stride(1) == 1, "key must be bf16 [N, 128] with a contiguous last dim")
+    _require(cache.dtype == torch.uint8 and cache.is_contiguous()
+             and cache.numel() % (page_size * INDEXER_ROW_BYTES) == 0, "cache must be contiguous uint8 pages")
+    slots, is64 = _slots(slot_mapping, key.shape[0])
+    dev = _check_cuda(key, cache, slots)
+    _lib.call("dsa_indexer_k_store", key.data_ptr(), key.stride(0), slots.data_ptr(), is64, key.shape[0],
+              cache.data_ptr(), int(page_size), _stream(dev))
