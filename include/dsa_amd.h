@@ -149,7 +149,10 @@ DSA_API size_t dsa_sparse_mla_workspace_bytes(int num_tokens, int num_heads, int
  *   q        [num_tokens, num_heads, 576] bf16, row stride q_token_stride,
  *            head stride q_head_stride (elements; last dim contiguous)
  *   kv_cache block b row r at kv_cache + b*kv_block_stride_bytes + r*656:
- *            [512 e4m3fn][4 x f32 tile scale][64 x bf16 rope]
+ *            [512 e4m3fn][4 x f32 tile scale][64 x bf16 rope]; the tile
+ *            scales are powers of two, as the reference's writer produces
+ *            (2^ceil(log2(amax/448)), fp8_utils.py:32-108) and the kernel
+ *            reads them as E8M0 exponents
  *   indices  [num_tokens, topk] int32 physical slots (block*kv_block_size+row),
  *            row stride idx_stride, -1 = skip
  *   out      [num_tokens, num_heads, 512] bf16, contiguous

@@ -8,6 +8,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -21,16 +22,24 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-fvisibility=hidden",
     "-Wall",
     "-Wno-unused-result",
     # No packed-fp32 instructions in device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA results in VGPRs: the accumulators feed VALU work (ReLU, softmax,
-    # rescale) every block, and AGPR-resident results cost a copy each time.
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
+# MFMA results in VGPRs where the accumulators feed VALU work (ReLU, top-k
+# keys) every step and AGPR-resident results would cost a copy each time. The
+# sparse-MLA kernel keeps its output accumulators in AGPRs instead: with 1 wave
+# per SIMD it needs more than the 256 architectural VGPRs.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+PER_FILE_FLAGS = {
+    "capi.hip": VGPR_FORM,
+    "topk.hip": VGPR_FORM,
+    "indexer.hip": VGPR_FORM,
+    "cache_store.hip": VGPR_FORM,
+    "sparse_mla.hip": [],
+}
 
 
 def hipcc() -> str:
@@ -38,9 +47,7 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source for gfx950 and link the shared library."""
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(LIB_PATH), *[str(CSRC / s) for s in SOURCES]]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -50,6 +57,19 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source for gfx950 (in parallel) and link the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    with tempfile.TemporaryDirectory(prefix="dsa_build_") as tmp:
+        objs = [os.path.join(tmp, Path(s).stem + ".o") for s in SOURCES]
+        cmds = [[hipcc(), *HIPCC_FLAGS, *PER_FILE_FLAGS[s], "-c", str(CSRC / s), "-o", o]
+                for s, o in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
+            list(pool.map(lambda c: _run(c, verbose), cmds))
+        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(LIB_PATH), *objs], verbose)
     return LIB_PATH
 
 

@@ -5,26 +5,41 @@
 //   o   = softmax(s) @ kv(idx)[:, :512],  lse = log(sum_i exp(s_i))
 // where kv(slot) is a 656-byte row [512 e4m3fn][4 x f32 tile scale][64 bf16].
 //
-// Workgroup = 4 waves = 64 heads of one token over one key split; each wave
-// owns 16 heads. Per block of 64 selected rows:
-//   load   : lane = row; wave w gathers tile w of the 64 rows (8 x 16 B fp8 +
-//            its f32 scale) and two 16 B rope chunks, a full block of compute
-//            ahead of use (the row indices one block further ahead);
-//   stage  : rows are dequantised in registers (fp8 * 2^k is exact in bf16,
-//            one v_cvt_scalef32_pk_bf16_fp8 per pair) and written once,
-//            row-major, into one of two LDS buffers [64][576] bf16 (double
-//            buffering: one barrier per block), between the QK MFMAs;
-//   QK     : S^T[64 keys x 16 heads] on v_mfma_f32_16x16x32_bf16, A = rows
-//            from LDS (four independent accumulator chains), B = the wave's
-//            16 query heads, resident in registers for the whole kernel;
-//   softmax: online in the exp2 domain, with lazy rescaling: the running max
-//            only moves (and O is only rescaled) when a block raises it by
-//            more than 2^8, so P stays in [0, 256] and the rescale is rare;
-//   PV     : O[16 heads x 512] += P . V, A = P straight from the QK
-//            accumulators (two 16-key C tiles form one 32-key A operand), B =
-//            V read from the same row-major LDS tile with ds_read_b64_tr_b16,
-//            which hands each 16-lane group a transposed 4-key x 16-dv tile -
-//            no separate transposed copy of V.
+// Workgroup = 4 waves = 64 heads of one token over one key split. The waves
+// form two pairs; a pair owns 32 heads and splits the work by dimension:
+// wave d of the pair contracts nope dims [256d, 256d+256) and rope dims
+// [32d, 32d+32) for the scores and produces output dims [256d, 256d+256).
+// Both halves of a score are summed through LDS, so each wave holds only its
+// half of the query (72 VGPRs) and of the output (128 accumulators).
+//
+// Per block of 64 selected rows:
+//   gather : the raw 656-byte rows go straight from HBM into LDS with
+//            global_load_lds_dwordx4 - consecutive lanes take consecutive
+//            16-byte pieces of the packed rows, so each load instruction
+//            touches ~10 cache lines instead of 64 - into one of three
+//            buffers, two blocks ahead of use. The row indices themselves
+//            arrive the same way, four blocks ahead, in a five-entry ring.
+//            Invalid indices read a zero row. No registers hold data in
+//            flight, so the prefetch depth costs only LDS. An LDS-bound load
+//            holds its wave until the address unit has taken it (~50 cycles
+//            each), so a wave sends its loads in runs of four that share one
+//            M0 value, after the block's MFMAs.
+//   QK     : S^T[64 keys x 32 heads]. The nope part runs on
+//            v_mfma_scale_f32_32x32x64_f8f6f4: A = the raw fp8 rows straight
+//            from LDS with the row's tile scale as the E8M0 block scale (the
+//            cache's scales are powers of two, so this is exact); B = the
+//            query as two fp8 terms hi + lo with per-chunk E8M0 scales, which
+//            together hold each bf16 query value to ~2^-22 of its chunk's
+//            largest. The rope part (bf16 in the row) runs on
+//            v_mfma_f32_32x32x16_bf16 against the bf16 query.
+//   softmax: partner partials summed, online softmax in the exp2 domain with
+//            lazy rescaling (the running max moves only when a block raises
+//            it by more than 2^8).
+//   PV     : O[32 heads x 256] += P' . V on v_mfma_f32_32x32x16_bf16. V comes from the
+//            raw rows with ds_read_b64_tr_b8 (8 keys x 1 dim per lane, the
+//            B operand layout) and is converted with unit scale; the per-row
+//            tile scale is folded into P instead (P' = P * 2^k, exact), and
+//            P' comes straight from the score accumulators.
 // Splits over the key list (for small batches) write normalised partial
 // outputs and LSEs to a caller-provided workspace; a combine kernel merges
 // them with the LSE rule of merge_attention_states.
@@ -35,23 +50,33 @@
 
 namespace dsa {
 
-typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 constexpr int kMlaThreads = 256;
 constexpr int kMlaHeadsPerWG = 64;
-constexpr int kMlaKeys = 64;            // rows per block
+constexpr int kMlaKeys = 64;              // rows per block
 constexpr int kMlaRowBytes = 656;
-constexpr int kMlaDqk = 576;
+constexpr int kMlaRowPieces = kMlaRowBytes / 16;      // 41
 constexpr int kMlaDv = 512;
-// Staged row pitch: 576 bf16 + 32 B. 296 dwords is an odd multiple of 8
-// banks, so 8 consecutive rows' 32-byte segments cover all 64 banks.
-constexpr int kPitch = kMlaDqk * 2 + 32;
-constexpr int kBufBytes = kMlaKeys * kPitch;
-constexpr size_t kMlaSmemBytes = 2 * (size_t)kBufBytes;
+constexpr int kBufBytes = kMlaKeys * kMlaRowBytes;    // 41984: one block of packed raw rows
+constexpr int kDmaPerBlock = kBufBytes / 1024;        // 41 wave-wide 16-byte loads
+constexpr int kNumBufs = 3;
+constexpr int kXchgOff = kNumBufs * kBufBytes;         // partial scores, 8 KB per wave
+constexpr int kSclOff = kXchgOff + 4 * 8192;           // per-wave row scales [2 tiles][64 keys]
+constexpr int kRingOff = kSclOff + 4 * 512;            // row indices, one 64-entry block per slot
+constexpr int kRingSlots = 5;
+constexpr size_t kMlaSmemBytes = kRingOff + kRingSlots * 256;  // 162048
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
+
+static_assert(kBufBytes % 1024 == 0, "a block of rows must be whole wave-wide loads");
+static_assert(kMlaSmemBytes <= 160 * 1024, "LDS budget");
+
+// Source of the pieces of an invalid row: 656 zero bytes.
+__device__ __align__(16) uint8_t g_mla_zero_row[kMlaRowBytes];
 
 struct MlaParams {
   const uint16_t* q;
@@ -59,6 +84,7 @@ struct MlaParams {
   const uint8_t* kv;
   int64_t kv_blk_stride;
   int kv_block_size;
+  int kv_block_shift;  // log2(kv_block_size) when it is a power of two, else -1
   const int32_t* idx;
   int64_t idx_stride;
   int T, H, topk, splits, head_groups;
@@ -69,59 +95,30 @@ struct MlaParams {
   float* ws_lse;  // [splits, T, H]
 };
 
-struct RowRegs {
-  v4i nope[8];   // this wave's 128-dim tile of the lane's row
-  v4i rope[2];   // rope chunks 2w, 2w+1
-  float scale;
-  bool valid;
-};
-
-__device__ __forceinline__ int32_t load_slot(const MlaParams& P, int t, int key0, int lane) {
-  return P.idx[(int64_t)t * P.idx_stride + key0 + lane];
+// ---- asynchronous global -> LDS copies. They are issued from inline asm so
+// that the compiler neither inserts vmcnt(0) before every LDS read nor waits
+// for them at barriers: the kernel counts them itself with wait_vm().
+// `lds` is the wave's destination base (M0); lane i writes lds + 4*size*i.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+// Wait until at most n of this wave's copies are outstanding (n in {0, 10, 11}).
+__device__ __forceinline__ void wait_vm(int n) {
+  if (n >= 11) asm volatile("s_waitcnt vmcnt(11)" ::: "memory");
+  else if (n == 10) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ void barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Gather this wave's share of the lane's row (`slot` < 0: an invalid index, zeros).
-__device__ __forceinline__ void load_rows(RowRegs& rr, const MlaParams& P, int32_t slot, int wave) {
-  rr.valid = slot >= 0;
-  if (rr.valid) {
-    const uint8_t* row = P.kv + (int64_t)(slot / P.kv_block_size) * P.kv_blk_stride +
-                         (int64_t)(slot % P.kv_block_size) * kMlaRowBytes;
-    const v4i* nope = reinterpret_cast<const v4i*>(row + wave * 128);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rr.nope[i] = nope[i];
-    rr.scale = reinterpret_cast<const float*>(row + 512)[wave];
-    const v4i* rope = reinterpret_cast<const v4i*>(row + 528 + wave * 32);
-    rr.rope[0] = rope[0];
-    rr.rope[1] = rope[1];
-  } else {
-    const v4i z = {0, 0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rr.nope[i] = z;
-    rr.rope[0] = z;
-    rr.rope[1] = z;
-    rr.scale = 0.f;
-  }
-}
-
-// Stage piece i (0-7: a 16-dim nope chunk of the wave's tile; 8: the wave's
-// two rope chunks) of the lane's row into the bf16 tile.
-__device__ __forceinline__ void stage_piece(const RowRegs& rr, uint8_t* buf, int lane, int wave, int i) {
-  uint8_t* krow = buf + lane * kPitch;
-  if (i < 8) {
-    const int c = wave * 8 + i;  // dims 16c .. 16c+15
-    v4i lo, hi;
-    dequant16_fp8_bf16(rr.nope[i], rr.scale, lo, hi);
-    *reinterpret_cast<v4i*>(krow + c * 32) = lo;
-    *reinterpret_cast<v4i*>(krow + c * 32 + 16) = hi;
-  } else {
-    *reinterpret_cast<v4i*>(krow + 1024 + wave * 32) = rr.rope[0];
-    *reinterpret_cast<v4i*>(krow + 1024 + wave * 32 + 16) = rr.rope[1];
-  }
-}
-
-__device__ __forceinline__ void stage_rows(const RowRegs& rr, uint8_t* buf, int lane, int wave) {
-#pragma unroll
-  for (int i = 0; i < 9; ++i) stage_piece(rr, buf, lane, wave, i);
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>(p);
 }
 
 __device__ __forceinline__ v8bf as_v8bf(v4i x) { return __builtin_bit_cast(v8bf, x); }
@@ -131,17 +128,172 @@ __device__ __forceinline__ int cvt_pk_bf16(float a, float b) {
   return __builtin_bit_cast(int, __builtin_convertvector(x, v2bf));
 }
 
-__device__ __forceinline__ v4s lds_read_tr16(const uint8_t* p) {
-  typedef __attribute__((address_space(3))) v4s lds_v4s;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p);
+__device__ __forceinline__ v2i lds_read_tr8(const uint8_t* p) {
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)p);
 }
 
-__global__ void __launch_bounds__(kMlaThreads)
+__device__ __forceinline__ v2i lds_read_tr8_at(uint32_t a) {
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(uintptr_t)a);
+}
+
+// Eight fp8 bytes (one per key) -> the bf16 B operand, unit scale.
+__device__ __forceinline__ v8bf fp8x8_to_bf16(v2i raw) {
+  v4i r;
+  r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[0], 1.f, false));
+  r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[0], 1.f, true));
+  r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[1], 1.f, false));
+  r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[1], 1.f, true));
+  return as_v8bf(r);
+}
+
+// E8M0 exponent (biased) of 2^(ceil(log2 v) - 8) for v >= 0: v * 2^-e stays
+// within +-256, inside the e4m3 range. Exact bit arithmetic; v = 0 gives 2^0.
+__device__ __forceinline__ int e8m0_for(float v) {
+  const uint32_t u = __float_as_uint(v);
+  if (u == 0u) return 127;
+  int e = (int)((u >> 23) & 0xffu);
+  const uint32_t m = u & 0x7fffffu;
+  int cl;  // ceil(log2 v)
+  if (e == 0) cl = (32 - __clz(m)) - 149 - ((m & (m - 1)) ? 0 : 1);
+  else cl = e - 127 + (m ? 1 : 0);
+  return min(max(cl - 8 + 127, 1), 254);
+}
+__device__ __forceinline__ float e8m0_value(int e) { return __uint_as_float((uint32_t)e << 23); }
+__device__ __forceinline__ float e8m0_inv(int e) { return __uint_as_float((uint32_t)(254 - e) << 23); }
+
+// Four floats -> four e4m3fn bytes (round to nearest even).
+__device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+__device__ __forceinline__ v8i lds_read32(const uint8_t* p) {
+  const v4i a = *reinterpret_cast<const v4i*>(p);
+  const v4i b = *reinterpret_cast<const v4i*>(p + 16);
+  v8i r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+// D = A . B + C on v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 x e4m3), with the
+// E8M0 scales taken from byte `sa_byte` of sa and byte `sb_byte` of sb. A lane
+// (row i, half h) holds k = 16h + 0..15 in bytes 0-15 and k = 32 + 16h + 0..15 in
+// bytes 16-31; the scale of k-block b of row i is read from lane 32b + i.
+template <int kSaByte, int kSbByte>
+__device__ __forceinline__ v16f mfma_fp8_32(v8i a, v8i b, v16f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, kSaByte, sa, kSbByte, sb);
+}
+// chunk c of a wave's 256 nope dims: row-scale byte c/2 (tile 2d + c/2), query-scale byte c
+__device__ __forceinline__ v16f mfma_fp8_chunk(int c, v8i a, v8i b, v16f acc, int sa, int sb) {
+  switch (c) {
+    case 0: return mfma_fp8_32<0, 0>(a, b, acc, sa, sb);
+    case 1: return mfma_fp8_32<0, 1>(a, b, acc, sa, sb);
+    case 2: return mfma_fp8_32<1, 2>(a, b, acc, sa, sb);
+    default: return mfma_fp8_32<1, 3>(a, b, acc, sa, sb);
+  }
+}
+
+// The gather of one block: prep_rows() reads the row indices from ring slot
+// j % 5 and forms each lane's row address; issue_all() sends this wave's loads.
+struct RowDma {
+  uint64_t rowp;  // this lane's row (lane = row of the block)
+  uint32_t lbuf;
+  int ln;         // lane id, opaque to the compiler (see prep_rows)
+  bool on;
+};
+
+// Wave w sends loads [first(w), first(w) + count(w)) of the block: 11 for wave 0,
+// 10 for the others, in runs of four that share one M0 (LDS base) value.
+__device__ __forceinline__ int dma_first(int wave) { return wave == 0 ? 0 : 1 + 10 * wave; }
+__device__ __forceinline__ int dma_count(int wave) { return wave == 0 ? 11 : 10; }
+
+__device__ __forceinline__ uint64_t row_dma_addr(const RowDma& g, int i) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = 64 * (dma_first(wave) + i) + g.ln;  // 16-byte piece of the packed block
+  const int r = min(c / kMlaRowPieces, kMlaKeys - 1);
+  const int piece = c - r * kMlaRowPieces;
+  return __shfl(g.rowp, r, 64) + 16 * piece;
+}
+
+__device__ __forceinline__ void prep_rows(RowDma& g, const MlaParams& P, const uint8_t* smem, int j,
+                                          const uint8_t* buf, int lane, bool on) {
+  g.on = on;
+  if (!on) return;
+  const int32_t slot = reinterpret_cast<const int32_t*>(smem + kRingOff + (j % kRingSlots) * 256)[lane];
+  if (slot >= 0) {
+    int64_t blk, in_blk;
+    if (P.kv_block_shift >= 0) {
+      blk = slot >> P.kv_block_shift;
+      in_blk = slot & ((1 << P.kv_block_shift) - 1);
+    } else {
+      blk = slot / P.kv_block_size;
+      in_blk = slot % P.kv_block_size;
+    }
+    g.rowp = reinterpret_cast<uint64_t>(P.kv + blk * P.kv_blk_stride + in_blk * kMlaRowBytes);
+  } else {
+    g.rowp = reinterpret_cast<uint64_t>(g_mla_zero_row);
+  }
+  g.lbuf = __builtin_amdgcn_readfirstlane(lds_addr(buf));
+  // an opaque lane id keeps the per-load lane offsets from being hoisted out
+  // of the block loop, where they would pin ~30 VGPRs for the whole kernel
+  g.ln = lane;
+  asm volatile("" : "+v"(g.ln));
+}
+
+// Send loads i .. i+n-1 (n <= 4) of this wave with one M0 value: the
+// immediate offset moves both the global and the LDS address by 1 KB steps.
+__device__ __forceinline__ void issue_run(const RowDma& g, int i, int n, int wave) {
+  if (!g.on) return;
+  const uint32_t m0 = g.lbuf + 1024 * (dma_first(wave) + i);
+  const uint64_t a0 = row_dma_addr(g, i);
+  const uint64_t a1 = row_dma_addr(g, i + 1) - 1024;
+  const uint64_t a2 = row_dma_addr(g, i + 2) - 2048;
+  const uint64_t a3 = row_dma_addr(g, i + 3) - 3072;
+  const uint32_t m = __builtin_amdgcn_readfirstlane(m0);
+  if (n == 4)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024\n\t"
+                 "global_load_lds_dwordx4 %2, off offset:2048\n\tglobal_load_lds_dwordx4 %3, off offset:3072"
+                 ::"v"(a0), "v"(a1), "v"(a2), "v"(a3), "{m0}"(m) : "memory");
+  else if (n == 3)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024\n\t"
+                 "global_load_lds_dwordx4 %2, off offset:2048"
+                 ::"v"(a0), "v"(a1), "v"(a2), "{m0}"(m) : "memory");
+  else if (n == 2)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024"
+                 ::"v"(a0), "v"(a1), "{m0}"(m) : "memory");
+}
+
+// All of this wave's loads of the block: 4 + 4 + 3 (wave 0) or 4 + 4 + 2.
+__device__ __forceinline__ void issue_all(const RowDma& g, int wave) {
+  issue_run(g, 0, 4, wave);
+  issue_run(g, 4, 4, wave);
+  issue_run(g, 8, dma_count(wave) - 8, wave);
+}
+
+__device__ __forceinline__ void issue_rows(const MlaParams& P, const uint8_t* smem, int j, uint8_t* buf,
+                                           int lane, int wave) {
+  RowDma g;
+  prep_rows(g, P, smem, j, buf, lane, true);
+  issue_all(g, wave);
+}
+
+__device__ __forceinline__ void issue_index(const MlaParams& P, uint8_t* smem, int t, int key_begin, int j,
+                                            int lane) {
+  const int32_t* src = P.idx + (int64_t)t * P.idx_stride + key_begin + j * kMlaKeys + lane;
+  dma4(src, __builtin_amdgcn_readfirstlane(lds_addr(smem + kRingOff + (j % kRingSlots) * 256)));
+}
+
+__global__ void __launch_bounds__(kMlaThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 sparse_mla_kernel(const MlaParams P) {
   extern __shared__ __align__(16) uint8_t smem[];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, c16 = lane & 15;
+  const int h = lane >> 5, c32 = lane & 31;
+  const int pair = wave >> 1, d = wave & 1;
 
   // XCD-aware order: consecutive logical work items (the head groups and
   // splits of one token) land on the same XCD and share its L2.
@@ -157,176 +309,317 @@ sparse_mla_kernel(const MlaParams P) {
   const int key_begin = split * chunk;
   const int nblk = chunk / kMlaKeys;
 
-  const int h0 = hg * kMlaHeadsPerWG + wave * 16;
-  const bool active = h0 < P.H;
+  const int h_pair = hg * kMlaHeadsPerWG + pair * 32;  // first head of the pair
+  const int head = h_pair + c32;                       // this lane's head (score columns)
+  const bool head_ok = head < P.H;
 
-  // Query heads as B operands of S^T = K . Q^T: head h0 + lane%16, dims ks*32 + g*8 .. +8.
-  v4i qb[18];
-  if (active) {
-    const uint16_t* qh = P.q + (int64_t)t * P.q_tok_stride + (int64_t)(h0 + c16) * P.q_head_stride + g * 8;
+  // Query B operands. Nope chunk c (dims 256d + 64c + 32h + 0..31 for lane half
+  // h) as two fp8 terms q = 2^e_hi * hi + 2^e_lo * lo with one E8M0 exponent per
+  // (head, 64-dim chunk): hi takes the top 4 significant bits of each bf16
+  // value and lo the rest, so the pair holds q to ~2^-22 of the chunk's
+  // largest value (bf16 has 8 significant bits; e4m3 normals span 2^15).
+  // Rope k-step rho: bf16 dims 32d + 16rho + 8h + 0..7.
+  v8i qhi[4], qlo[4];
+  int qe_hi = 0, qe_lo = 0;  // byte c: biased exponent of chunk c
+  v4i qr[2];
+  {
+    const uint16_t* qh = P.q + (int64_t)t * P.q_tok_stride + (int64_t)(head_ok ? head : 0) * P.q_head_stride;
+    const v4i z = {0, 0, 0, 0};
 #pragma unroll
-    for (int ks = 0; ks < 18; ++ks) qb[ks] = *reinterpret_cast<const v4i*>(qh + ks * 32);
+    for (int c = 0; c < 4; ++c) {
+      const uint16_t* p = qh + 256 * d + 64 * c + 32 * h;
+      float x[32];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4i w = head_ok ? *reinterpret_cast<const v4i*>(p + 8 * i) : z;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[8 * i + 2 * e] = __uint_as_float((uint32_t)w[e] << 16);
+          x[8 * i + 2 * e + 1] = __uint_as_float((uint32_t)w[e] & 0xffff0000u);
+        }
+      }
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+      amax = fmaxf(amax, shfl_xor(amax, 32));
+      const int ehi = e8m0_for(amax);
+      const float inv_hi = e8m0_inv(ehi);
+      const float s_hi = e8m0_value(ehi);
+      float r[32];
+      float rmax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; i += 4) {
+        const uint32_t w = f32x4_to_fp8(x[i] * inv_hi, x[i + 1] * inv_hi, x[i + 2] * inv_hi, x[i + 3] * inv_hi);
+        qhi[c][i / 4] = (int)w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const v2f dq = fp8x2_to_f32(w >> (16 * (e >> 1)), false);
+          r[i + e] = x[i + e] - dq[e & 1] * s_hi;  // exact
+          rmax = fmaxf(rmax, fabsf(r[i + e]));
+        }
+      }
+      rmax = fmaxf(rmax, shfl_xor(rmax, 32));
+      const int elo = e8m0_for(rmax);
+      const float inv_lo = e8m0_inv(elo);
+#pragma unroll
+      for (int i = 0; i < 32; i += 4)
+        qlo[c][i / 4] = (int)f32x4_to_fp8(r[i] * inv_lo, r[i + 1] * inv_lo, r[i + 2] * inv_lo, r[i + 3] * inv_lo);
+      qe_hi |= ehi << (8 * c);
+      qe_lo |= elo << (8 * c);
+    }
+#pragma unroll
+    for (int rho = 0; rho < 2; ++rho)
+      qr[rho] = head_ok ? *reinterpret_cast<const v4i*>(qh + 512 + 32 * d + 16 * rho + 8 * h) : z;
   }
+  // The query must be in registers before the first copy is issued: a wait
+  // the compiler places for these loads inside the block loop would also wait
+  // for every copy in flight. (The builtin, unlike inline asm, is seen by the
+  // compiler's wait bookkeeping.) 0x0f70 = vmcnt(0) only.
+  __builtin_amdgcn_s_waitcnt(0x0f70);
 
-  // o[dt][r]: head h0 + 4g + r, dv dt*16 + c16
-  v4f o[32];
+  v16f o[8];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) o[i] = (v4f){0.f, 0.f, 0.f, 0.f};
-  float m_run = -__builtin_inff();  // per head c16, log2 domain
-  float l_run = 0.f;                // per head c16, this lane's keys only
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float m_run = -__builtin_inff();  // per head c32, log2 domain
+  float l_run = 0.f;                // per head c32, this lane half's keys only
 
-  // Pipeline: block n is multiplied from LDS while block n+1 (in registers)
-  // is staged into the other buffer and block n+2's rows are in flight; the
-  // row indices run one block further ahead.
-  RowRegs rr;
-  load_rows(rr, P, load_slot(P, t, key_begin, lane), wave);
-  int32_t slot_pf = nblk > 1 ? load_slot(P, t, key_begin + kMlaKeys, lane) : -1;
-  uint64_t vm_cur = __ballot(rr.valid);
-  stage_rows(rr, smem, lane, wave);
-  if (nblk > 1) load_rows(rr, P, slot_pf, wave);
-  if (nblk > 2) slot_pf = load_slot(P, t, key_begin + 2 * kMlaKeys, lane);
-  __syncthreads();
+  const int my_dma = wave == 0 ? 11 : 10;
+  // prologue: indices of blocks 0-3, then rows of blocks 0 and 1
+  if (wave == 1) {
+    for (int j = 0; j < 4 && j < nblk; ++j) issue_index(P, smem, t, key_begin, j, lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  barrier();
+  issue_rows(P, smem, 0, smem, lane, wave);
+  if (nblk > 1) issue_rows(P, smem, 1, smem + kBufBytes, lane, wave);
+
+  float* xmine = reinterpret_cast<float*>(smem + kXchgOff + wave * 8192);
+  const float* xpart = reinterpret_cast<const float*>(smem + kXchgOff + (wave ^ 1) * 8192);
+  float* scl = reinterpret_cast<float*>(smem + kSclOff + wave * 512);
 
   for (int n = 0; n < nblk; ++n) {
-    const uint8_t* buf = smem + (n & 1) * kBufBytes;
-    uint8_t* next_buf = smem + ((n + 1) & 1) * kBufBytes;
-    const bool stage_next = n + 1 < nblk;
-    const uint64_t vm_next = stage_next ? __ballot(rr.valid) : 0ull;
-    if (active && vm_cur) {
-      // ---- S^T = K . Q^T: s[kt][r] = score(key kt*16 + 4g + r, head c16).
-      // A operands are read two k-steps ahead of their MFMAs.
-      v4f s[4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) s[kt] = (v4f){0.f, 0.f, 0.f, 0.f};
-      const uint8_t* arow = buf + c16 * kPitch + g * 16;
-      v4i a[3][4];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) a[ks][kt] = *reinterpret_cast<const v4i*>(arow + kt * 16 * kPitch + ks * 64);
-#pragma unroll
-      for (int ks = 0; ks < 18; ++ks) {
-        if (ks + 2 < 18) {
-#pragma unroll
-          for (int kt = 0; kt < 4; ++kt)
-            a[(ks + 2) % 3][kt] = *reinterpret_cast<const v4i*>(arow + kt * 16 * kPitch + (ks + 2) * 64);
-        }
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-          s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a[ks % 3][kt]), as_v8bf(qb[ks]), s[kt], 0, 0, 0);
-        if (stage_next && (ks & 1)) stage_piece(rr, next_buf, lane, wave, ks >> 1);
-      }
-      // block n+1 is staged: its registers take block n+2's rows now, which
-      // leaves them a whole block of compute to arrive
-      if (n + 2 < nblk) {
-        load_rows(rr, P, slot_pf, wave);
-        if (n + 3 < nblk) slot_pf = load_slot(P, t, key_begin + (n + 3) * kMlaKeys, lane);
-      }
+    // rows of block n (and, for wave 1, the indices of block n+2) have landed
+    int allow = n + 1 < nblk ? my_dma : 0;
+    if (wave == 1 && n >= 1 && n + 3 < nblk) allow += 1;
+    wait_vm(allow);
+    barrier();
+    const uint8_t* buf = smem + (n % kNumBufs) * kBufBytes;
+    const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kRingOff + (n % kRingSlots) * 256)[lane];
+    const uint64_t vmask = __ballot(slot_n >= 0);
+    if (wave == 1 && n + 4 < nblk) issue_index(P, smem, t, key_begin, n + 4, lane);
+    // block n+2's rows go out between this block's MFMAs (loads 0-3 in QK, 4-10 in PV)
+    RowDma g;
+    prep_rows(g, P, smem, n + 2, smem + ((n + 2) % kNumBufs) * kBufBytes, lane, n + 2 < nblk);
 
-      // ---- online softmax (exp2 domain), lazy rescale
-      float mloc = -__builtin_inff();
+    // ---- partial S^T over this wave's dims: s[kt][r] = key 32kt + 8(r/4) + 4h + r%4, head c32
+    v16f s[2];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kt * 16 + g * 4 + r;
-          const float x = ((vm_cur >> key) & 1ull) ? s[kt][r] * P.scale_log2 : -__builtin_inff();
-          s[kt][r] = x;
-          mloc = fmaxf(mloc, x);
-        }
-      mloc = fmaxf(mloc, shfl_xor(mloc, 16));
-      mloc = fmaxf(mloc, shfl_xor(mloc, 32));
-      const bool need = mloc > m_run + kRescaleThreshold;  // true on the first valid block
-      if (__ballot(need)) {
-        const float m_new = need ? mloc : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
-        l_run *= alpha;
-        m_run = m_new;
+      for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
+    v2f ksc[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float ar = __shfl(alpha, g * 4 + r, 64);
+    for (int kt = 0; kt < 2; ++kt)
+      ksc[kt] = *reinterpret_cast<const v2f*>(buf + (32 * kt + c32) * kMlaRowBytes + 512 + 8 * d);
+    // E8M0 of the row's tile scales (powers of two): byte tt = tile 2d + tt
+    int ke[2];
 #pragma unroll
-          for (int dt = 0; dt < 32; ++dt) o[dt][r] *= ar;
-        }
+    for (int kt = 0; kt < 2; ++kt)
+      ke[kt] = (int)(((__float_as_uint(ksc[kt][0]) >> 23) & 0xffu) | (((__float_as_uint(ksc[kt][1]) >> 23) & 0xffu) << 8));
+    // K chunk c: lane half h holds bytes 256d + 64c + 32h .. +32 of key 32kt + c32
+    const uint8_t* krow = buf + c32 * kMlaRowBytes + 256 * d + 32 * h;
+    v8i kraw[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) kraw[0][kt] = lds_read32(krow + 32 * kt * kMlaRowBytes);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c + 1 < 4) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) kraw[(c + 1) & 1][kt] = lds_read32(krow + 32 * kt * kMlaRowBytes + 64 * (c + 1));
       }
-      float psum = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(s[kt][r] - m_run);
-          s[kt][r] = pv;
-          psum += pv;
-        }
-      l_run += psum;
-
-      // ---- O += P . V, V operands two tiles ahead
-      v4i pa[2];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        pa[kk][0] = cvt_pk_bf16(s[2 * kk][0], s[2 * kk][1]);
-        pa[kk][1] = cvt_pk_bf16(s[2 * kk][2], s[2 * kk][3]);
-        pa[kk][2] = cvt_pk_bf16(s[2 * kk + 1][0], s[2 * kk + 1][1]);
-        pa[kk][3] = cvt_pk_bf16(s[2 * kk + 1][2], s[2 * kk + 1][3]);
+      for (int kt = 0; kt < 2; ++kt) {
+        s[kt] = mfma_fp8_chunk(c, kraw[c & 1][kt], qhi[c], s[kt], ke[kt], qe_hi);
+        s[kt] = mfma_fp8_chunk(c, kraw[c & 1][kt], qlo[c], s[kt], ke[kt], qe_lo);
       }
-      // lane (g, c16) addresses key row 4g + c16/4 (+16, +32, +48), dv 4*(c16%4) of each 16-dv tile
-      const uint8_t* vb = buf + (4 * g + (c16 >> 2)) * kPitch + (c16 & 3) * 8;
-      v4s vv[3][4];
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
+    for (int rho = 0; rho < 2; ++rho)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) vv[dt][q] = lds_read_tr16(vb + q * 16 * kPitch + dt * 32);
-#pragma unroll
-      for (int dt = 0; dt < 32; ++dt) {
-        if (dt + 2 < 32) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) vv[(dt + 2) % 3][q] = lds_read_tr16(vb + q * 16 * kPitch + (dt + 2) * 32);
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const v8bf bop = __builtin_bit_cast(
-              v8bf, __builtin_shufflevector(vv[dt % 3][2 * kk], vv[dt % 3][2 * kk + 1], 0, 1, 2, 3, 4, 5, 6, 7));
-          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(pa[kk]), bop, o[dt], 0, 0, 0);
-        }
+      for (int kt = 0; kt < 2; ++kt) {
+        const v4i rope = *reinterpret_cast<const v4i*>(buf + (32 * kt + c32) * kMlaRowBytes + 528 + 64 * d +
+                                                       32 * rho + 16 * h);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(rope), as_v8bf(qr[rho]), s[kt], 0, 0, 0);
       }
-    } else {
-      if (stage_next) stage_rows(rr, next_buf, lane, wave);
-      if (n + 2 < nblk) {
-        load_rows(rr, P, slot_pf, wave);
-        if (n + 3 < nblk) slot_pf = load_slot(P, t, key_begin + (n + 3) * kMlaKeys, lane);
+    // this wave's row scales, by key, for folding into P
+    if (h == 0) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        scl[32 * kt + c32] = ksc[kt][0];
+        scl[64 + 32 * kt + c32] = ksc[kt][1];
       }
     }
-    __syncthreads();
-    vm_cur = vm_next;
+
+    // ---- exchange partial scores with the partner wave
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const v4f v = {s[q >> 2][4 * (q & 3)], s[q >> 2][4 * (q & 3) + 1], s[q >> 2][4 * (q & 3) + 2],
+                     s[q >> 2][4 * (q & 3) + 3]};
+      *reinterpret_cast<v4f*>(xmine + q * 256 + lane * 4) = v;
+    }
+    barrier();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const v4f v = *reinterpret_cast<const v4f*>(xpart + q * 256 + lane * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[q >> 2][4 * (q & 3) + e] += v[e];
+    }
+
+    // ---- online softmax (exp2 domain), lazy rescale
+    float mloc = -__builtin_inff();
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kt][r] *= P.scale_log2;
+    if (vmask != ~0ull) {
+      // invalid keys score -inf; their rows are zeros, so P . V gets exact zeros
+      const uint64_t vm = vmask >> (4 * h);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (!((vm >> (32 * kt + 8 * (r >> 2) + (r & 3))) & 1ull)) s[kt][r] = -__builtin_inff();
+    }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kt][r]);
+    mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+    const bool need = mloc > m_run + kRescaleThreshold;  // true on the first valid block
+    if (__ballot(need)) {
+      const float m_new = need ? mloc : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
+      l_run *= alpha;
+      m_run = m_new;
+      // o rows are heads 8(r/4) + 4h + r%4
+      int hh = 4 * h;
+      asm volatile("" : "+v"(hh));
+      float ar[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ar[r] = __shfl(alpha, 8 * (r >> 2) + hh + (r & 3), 64);
+      // one output tile at a time: the accumulators live in AGPRs
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[nt][r] *= ar[r];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // m_run is -inf only while every key so far was invalid; then p = 0
+    const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
+    float psum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(s[kt][r] - m_use);
+        s[kt][r] = pv;
+        psum += pv;
+      }
+    l_run += psum;
+
+    // ---- O += P' . V. Lane (group G = lane/16, m = lane%16) addresses key row
+    // 8(e/4) + 4h + e%4 (e = m/2) and dims (G%2)*16 + 8(m%2) of each 32-dim tile.
+    const int m16 = lane & 15, G = lane >> 4;
+    const int e8 = m16 >> 1;
+    const uint8_t* vb = buf + (8 * (e8 >> 2) + 4 * h + (e8 & 3)) * kMlaRowBytes + 256 * d + (G & 1) * 16 +
+                        8 * (m16 & 1);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      // P' for row-scale tile 2d + tt: element e of k-step (kt, j) is key 32kt + 16j + 8(e/4) + 4h + e%4
+      v4i pa[2][2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v4f sa = *reinterpret_cast<const v4f*>(scl + 64 * tt + 32 * kt + 16 * j + 4 * h);
+          const v4f sb = *reinterpret_cast<const v4f*>(scl + 64 * tt + 32 * kt + 16 * j + 8 + 4 * h);
+          pa[kt][j][0] = cvt_pk_bf16(s[kt][8 * j + 0] * sa[0], s[kt][8 * j + 1] * sa[1]);
+          pa[kt][j][1] = cvt_pk_bf16(s[kt][8 * j + 2] * sa[2], s[kt][8 * j + 3] * sa[3]);
+          pa[kt][j][2] = cvt_pk_bf16(s[kt][8 * j + 4] * sb[0], s[kt][8 * j + 5] * sb[1]);
+          pa[kt][j][3] = cvt_pk_bf16(s[kt][8 * j + 6] * sb[2], s[kt][8 * j + 7] * sb[3]);
+        }
+      // The transposing reads take no immediate offset, so each address is
+      // formed from an opaque base right before use; otherwise all 32 would be
+      // hoisted out of the block loop into registers.
+      auto vtile = [&](int nt) {
+        uint32_t a = lds_addr(vb) + 32 * nt;
+        asm volatile("" : "+v"(a));
+        return a;
+      };
+      v2i vr[2][4];
+      {
+        const uint32_t p = vtile(4 * tt);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) vr[0][ks] = lds_read_tr8_at(p + (16 * ks) * kMlaRowBytes);
+      }
+#pragma unroll
+      for (int nn = 0; nn < 4; ++nn) {
+        if (nn + 1 < 4) {
+          const uint32_t p = vtile(4 * tt + nn + 1);
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) vr[(nn + 1) & 1][ks] = lds_read_tr8_at(p + (16 * ks) * kMlaRowBytes);
+        }
+        const int nt = 4 * tt + nn;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa[ks >> 1][ks & 1]),
+                                                          fp8x8_to_bf16(vr[nn & 1][ks]), o[nt], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // block n+2's rows: an LDS-bound copy holds its wave until the address
+    // unit has taken it, so all of them go out after this block's MFMAs
+    issue_all(g, wave);
   }
 
-  if (!active) return;
-  l_run += shfl_xor(l_run, 16);
+  // drain: nothing may be left in flight when the workgroup ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (h_pair >= P.H) return;
   l_run += shfl_xor(l_run, 32);
   const bool any = l_run > 0.f;
   const float inv = any ? 1.f / l_run : 0.f;
   const float lse = any ? (m_run + __builtin_amdgcn_logf(l_run)) * kLn2 : -__builtin_inff();
-  float inv_r[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) inv_r[r] = __shfl(inv, g * 4 + r, 64);
-
+  // o[nt][r]: head h_pair + 8(r/4) + 4h + r%4, dim 256d + 32nt + c32
   if (P.splits == 1) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      uint16_t* orow = P.out + ((int64_t)t * P.H + h0 + g * 4 + r) * kMlaDv + c16;
+    for (int r = 0; r < 16; ++r) {
+      const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
+      const float ir = __shfl(inv, hr, 64);
+      if (h_pair + hr < P.H) {
+        uint16_t* orow = P.out + ((int64_t)t * P.H + h_pair + hr) * kMlaDv + 256 * d + c32;
 #pragma unroll
-      for (int dt = 0; dt < 32; ++dt) orow[dt * 16] = (uint16_t)f32_to_bf16_rne(o[dt][r] * inv_r[r]);
+        for (int nt = 0; nt < 8; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
+      }
     }
-    if (g == 0 && P.lse) P.lse[(int64_t)t * P.H + h0 + c16] = lse;
+    if (h == 0 && d == 0 && head_ok && P.lse) P.lse[(int64_t)t * P.H + head] = lse;
   } else {
-    const int64_t row0 = ((int64_t)split * P.T + t) * P.H + h0;
+    const int64_t row0 = ((int64_t)split * P.T + t) * P.H + h_pair;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float* orow = P.ws_o + (row0 + g * 4 + r) * kMlaDv + c16;
+    for (int r = 0; r < 16; ++r) {
+      const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
+      const float ir = __shfl(inv, hr, 64);
+      if (h_pair + hr < P.H) {
+        float* orow = P.ws_o + (row0 + hr) * kMlaDv + 256 * d + c32;
 #pragma unroll
-      for (int dt = 0; dt < 32; ++dt) orow[dt * 16] = o[dt][r] * inv_r[r];
+        for (int nt = 0; nt < 8; ++nt) orow[32 * nt] = o[nt][r] * ir;
+      }
     }
-    if (g == 0) P.ws_lse[row0 + c16] = lse;
+    if (h == 0 && d == 0 && head_ok) P.ws_lse[row0 + c32] = lse;
   }
 }
 
@@ -429,6 +722,7 @@ int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_
   if (smem_status) return set_error(kLaunchFailed, "sparse_mla: cannot reserve %zu B of LDS", kMlaSmemBytes);
 
   MlaParams P;
+  P.kv_block_shift = (kv_block_size & (kv_block_size - 1)) == 0 ? __builtin_ctz((unsigned)kv_block_size) : -1;
   P.q = static_cast<const uint16_t*>(q);
   P.q_tok_stride = q_token_stride;
   P.q_head_stride = q_head_stride;

@@ -1,8 +1,10 @@
 """Sparse MLA decode on the GPU vs the CPU oracle.
 
 Tolerances (north star): o within bf16 atol 2e-2, LSE within 1e-3 (absolute,
-natural log). The rows' fp8 values dequantise exactly into bf16, so the only
-differences are bf16 rounding of P and fp32 accumulation order.
+natural log). The rows' fp8 values times their power-of-two tile scales are
+exact in the MFMA inputs; the query enters the fp8 score MFMA as two fp8 terms
+that hold it to ~2^-22 of each 64-dim chunk's largest value. The remaining
+differences are the bf16 rounding of P and the fp32 accumulation order.
 """
 import numpy as np
 import pytest
