@@ -61,7 +61,7 @@ constexpr int kMlaRowBytes = 656;
 constexpr int kMlaRowPieces = kMlaRowBytes / 16;      // 41
 constexpr int kMlaDv = 512;
 constexpr int kBufBytes = kMlaKeys * kMlaRowBytes;    // 41984: one block of packed raw rows
-constexpr int kDmaPerBlock = kBufBytes / 1024;        // 41 wave-wide 16-byte loads
+constexpr int kDmaPerBlock = kBufBytes / 1024;        // 41 wave-wide 16-byte loads per block
 constexpr int kNumBufs = 3;
 constexpr int kXchgOff = kNumBufs * kBufBytes;         // partial scores, 8 KB per wave
 constexpr int kSclOff = kXchgOff + 4 * 8192;           // per-wave row scales [2 tiles][64 keys]
@@ -208,8 +208,9 @@ struct RowDma {
 
 // Wave w sends loads [first(w), first(w) + count(w)) of the block: 11 for wave 0,
 // 10 for the others, in runs of four that share one M0 (LDS base) value.
-__device__ __forceinline__ int dma_first(int wave) { return wave == 0 ? 0 : 1 + 10 * wave; }
-__device__ __forceinline__ int dma_count(int wave) { return wave == 0 ? 11 : 10; }
+__device__ __forceinline__ int dma_count(int wave) { return kDmaPerBlock / 4 + (wave < kDmaPerBlock % 4 ? 1 : 0); }
+__device__ __forceinline__ int dma_first(int wave) { return wave * (kDmaPerBlock / 4) + min(wave, kDmaPerBlock % 4); }
+static_assert(kDmaPerBlock / 4 == 10 && kDmaPerBlock % 4 == 1, "wait_vm() counts 11 / 10 loads per wave");
 
 __device__ __forceinline__ uint64_t row_dma_addr(const RowDma& g, int i) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -385,7 +386,7 @@ sparse_mla_kernel(const MlaParams P) {
   float m_run = -__builtin_inff();  // per head c32, log2 domain
   float l_run = 0.f;                // per head c32, this lane half's keys only
 
-  const int my_dma = wave == 0 ? 11 : 10;
+  const int my_dma = dma_count(wave);
   // prologue: indices of blocks 0-3, then rows of blocks 0 and 1
   if (wave == 1) {
     for (int j = 0; j < 4 && j < nblk; ++j) issue_index(P, smem, t, key_begin, j, lane);
@@ -439,11 +440,11 @@ sparse_mla_kernel(const MlaParams P) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) kraw[(c + 1) & 1][kt] = lds_read32(krow + 32 * kt * kMlaRowBytes + 64 * (c + 1));
       }
+      // alternate the two accumulators so that no MFMA waits on its predecessor
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        s[kt] = mfma_fp8_chunk(c, kraw[c & 1][kt], qhi[c], s[kt], ke[kt], qe_hi);
-        s[kt] = mfma_fp8_chunk(c, kraw[c & 1][kt], qlo[c], s[kt], ke[kt], qe_lo);
-      }
+      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma_fp8_chunk(c, kraw[c & 1][kt], qhi[c], s[kt], ke[kt], qe_hi);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma_fp8_chunk(c, kraw[c & 1][kt], qlo[c], s[kt], ke[kt], qe_lo);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -555,30 +556,33 @@ sparse_mla_kernel(const MlaParams P) {
       // The transposing reads take no immediate offset, so each address is
       // formed from an opaque base right before use; otherwise all 32 would be
       // hoisted out of the block loop into registers.
-      auto vtile = [&](int nt) {
-        uint32_t a = lds_addr(vb) + 32 * nt;
+      // k-step outer, output tile inner: the four MFMAs of a k-step go to four
+      // different accumulators, so none waits for the previous one's result.
+      auto vstep = [&](int ks) {
+        uint32_t a = lds_addr(vb) + (16 * ks) * kMlaRowBytes + 32 * (4 * tt);
         asm volatile("" : "+v"(a));
         return a;
       };
       v2i vr[2][4];
       {
-        const uint32_t p = vtile(4 * tt);
+        const uint32_t p = vstep(0);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) vr[0][ks] = lds_read_tr8_at(p + (16 * ks) * kMlaRowBytes);
+        for (int nn = 0; nn < 4; ++nn) vr[0][nn] = lds_read_tr8_at(p + 32 * nn);
       }
 #pragma unroll
-      for (int nn = 0; nn < 4; ++nn) {
-        if (nn + 1 < 4) {
-          const uint32_t p = vtile(4 * tt + nn + 1);
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks + 1 < 4) {
+          const uint32_t p = vstep(ks + 1);
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) vr[(nn + 1) & 1][ks] = lds_read_tr8_at(p + (16 * ks) * kMlaRowBytes);
+          for (int nn = 0; nn < 4; ++nn) vr[(ks + 1) & 1][nn] = lds_read_tr8_at(p + 32 * nn);
         }
-        const int nt = 4 * tt + nn;
+        v8bf vb16[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa[ks >> 1][ks & 1]),
-                                                          fp8x8_to_bf16(vr[nn & 1][ks]), o[nt], 0, 0, 0);
-        }
+        for (int nn = 0; nn < 4; ++nn) vb16[nn] = fp8x8_to_bf16(vr[ks & 1][nn]);
+#pragma unroll
+        for (int nn = 0; nn < 4; ++nn)
+          o[4 * tt + nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa[ks >> 1][ks & 1]), vb16[nn],
+                                                                   o[4 * tt + nn], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
     }

@@ -468,6 +468,218 @@ topk_finish_kernel(const RowIn in, const RowWs* __restrict__ ws, const int32_t* 
   for (int i = tid; i < top_k; i += kTopkThreads) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
 }
 
+// ---------------------------------------------------------------- one launch
+// Rows of up to 64K positions: one 512-thread workgroup per row holds the
+// whole row in registers (128 order keys per thread), so every pass after the
+// one HBM read runs on registers and LDS:
+//   1. a 1/8 sample (every 8th register slot, spread over the row) gives the
+//      score threshold t by a two-digit radix, exactly as the threshold kernel;
+//   2. each thread counts its keys >= t; one block scan gives every thread its
+//      place in the candidate list, which goes to LDS in thread order;
+//   3. if the list holds between k and 4096 entries, the exact top-k is the
+//      exact top-k of the list (radix levels in LDS); otherwise the levels run
+//      over the registers (the same result without any bound);
+//   4. bitmap compaction in position order and the page translation.
+constexpr int kRegThreads = 512;
+constexpr int kRegPerThread = 128;
+constexpr int kRegMaxLen = kRegThreads * kRegPerThread;  // 65536
+
+// Position of register slot i of thread t (slot i = element i%4 of float4 chunk i/4).
+__device__ __forceinline__ int reg_pos(int t, int i) { return 4 * kRegThreads * (i >> 2) + 4 * t + (i & 3); }
+
+__global__ void __launch_bounds__(kRegThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const int32_t* __restrict__ page_table,
+                    int64_t pt_stride, uint32_t page_bits, int32_t* __restrict__ out_page,
+                    int32_t* __restrict__ out_raw, int top_k) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  TopkSmem& s = *reinterpret_cast<TopkSmem*>(smem_raw);
+  constexpr int NT = kRegThreads;
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int len = in.len(b);
+  const float* row = in.row(b);
+
+  RowOut out;
+  out.page = out_page + (int64_t)b * top_k;
+  out.raw = out_raw ? out_raw + (int64_t)b * top_k : nullptr;
+  out.pt = page_table ? page_table + (int64_t)b * pt_stride : nullptr;
+  out.page_bits = page_bits;
+  out.offset = offsets ? offsets[b] : 0;
+
+  if (len <= top_k) {
+    for (int i = tid; i < top_k; i += NT) out.emit(i, i < len ? i : -1);
+    return;
+  }
+
+  // ---- the row, as order keys (0 = beyond the row: below every real key).
+  // The launcher guarantees 16-byte aligned rows.
+  uint32_t key[kRegPerThread];
+  // Every load is in bounds: a chunk past the row's storage re-reads the
+  // row's last aligned chunk (len > top_k >= 4 here), and the keys of
+  // positions >= len are masked to 0, so no load sits behind a branch.
+  const int last = (int)((in.max_len - 4) & ~(int64_t)3);
+#pragma unroll
+  for (int j = 0; j < kRegPerThread / 4; ++j) {
+    const int p = 4 * kRegThreads * j + 4 * tid;
+    const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(row + min(p, last)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[4 * j + e] = p + e < len ? order_key(v[e]) : 0u;
+  }
+
+  const int nwords = (len + 31) >> 5;
+  for (int i = tid; i < nwords; i += NT) s.bitmap[i] = 0u;
+  for (int i = tid; i < kHistBins; i += NT) s.hist[i] = 0u;
+  if (tid < 2) s.list_count[tid] = 0u;
+  __syncthreads();
+
+  // ---- 1. threshold from the sample (slots 0, 8, 16, ...)
+  uint32_t my_samples = 0;
+#pragma unroll
+  for (int m = 0; m < kRegPerThread / 8; ++m)
+    if (key[8 * m]) {
+      atomicAdd(&s.hist[key[8 * m] >> 20], 1u);
+      ++my_samples;
+    }
+  uint32_t nsample = 0;
+  (void)block_exclusive_scan<NT>(s.wave_sum, my_samples, &nsample);
+  __syncthreads();
+  const float fk = (float)nsample / (float)len * (float)top_k;
+  const uint32_t r = (uint32_t)(fk + 4.f * sqrtf(fk) + 8.f);
+  uint32_t t_key = 1u;  // every real key is >= 0x007fffff
+  if (r < nsample) {
+    find_threshold<NT>(s.hist, s.wave_sum, 4096, r, &s.tb, &s.above, &s.eq);
+    const uint32_t tb0 = s.tb, rem0 = r - s.above;
+    __syncthreads();
+    for (int i = tid; i < 1024; i += NT) s.hist[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < kRegPerThread / 8; ++m)
+      if (key[8 * m] && (key[8 * m] >> 20) == tb0) atomicAdd(&s.hist[(key[8 * m] >> 10) & 1023u], 1u);
+    __syncthreads();
+    find_threshold<NT>(s.hist, s.wave_sum, 1024, rem0, &s.tb, &s.above, &s.eq);
+    t_key = max((tb0 << 20) | (s.tb << 10), 1u);
+  }
+
+  // ---- 2. candidates >= t, written in thread order after one block scan; a
+  // slot that no lane of the wave fills costs one compare and one ballot
+  uint32_t mine = 0;
+#pragma unroll
+  for (int i = 0; i < kRegPerThread; ++i) mine += key[i] >= t_key ? 1u : 0u;
+  uint32_t total_cand = 0;
+  uint32_t put = block_exclusive_scan<NT>(s.wave_sum, mine, &total_cand);
+  if (total_cand <= (uint32_t)kListCap) {
+    // positions recomputed here from an opaque thread id: computed once and
+    // kept, they would take as many registers as the keys
+    int t_o = tid;
+    uint32_t t_k = t_key;  // opaque too: the counting loop's compares are not kept
+    asm volatile("" : "+v"(t_o), "+v"(t_k));
+#pragma unroll
+    for (int i = 0; i < kRegPerThread; ++i) {
+      const bool pred = key[i] >= t_k;
+      if (__ballot(pred)) {
+        if (pred) {
+          s.list_key[0][put] = key[i];
+          s.list_pos[0][put] = (uint32_t)reg_pos(t_o, i);
+        }
+        put += pred ? 1u : 0u;
+      }
+    }
+  }
+  const uint32_t cand = total_cand;
+  const bool listed = cand >= (uint32_t)top_k && cand <= (uint32_t)kListCap;
+  for (int i = tid; i < kHistBins; i += NT) s.hist[i] = 0u;
+  __syncthreads();
+  if (listed) {
+    for (uint32_t e = tid; e < cand; e += NT) atomicAdd(&s.hist[s.list_key[0][e] >> 20], 1u);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRegPerThread; ++i)
+      if (key[i]) atomicAdd(&s.hist[key[i] >> 20], 1u);
+  }
+  __syncthreads();
+
+  // ---- 3. exact radix levels over the list (LDS) or, when the sample missed,
+  // over the row re-read from memory (the registers are free by then)
+  uint32_t thr[kLevels] = {0, 0, 0, 0, 0};
+  uint32_t remain = (uint32_t)top_k;
+  bool source_mode = !listed;
+  int cur = 0;
+  uint32_t list_n = listed ? cand : 0u;
+  for (int level = 0; level < kLevels; ++level) {
+    find_threshold<NT>(s.hist, s.wave_sum, radix_bins(level), remain, &s.tb, &s.above, &s.eq);
+    const uint32_t tb = s.tb, above = s.above, eq = s.eq;
+    thr[level] = tb;
+    remain -= above;
+    const bool take_all = (eq == remain) || level == kLevels - 1;
+    const bool collect = !take_all && (!source_mode || eq <= (uint32_t)kListCap);
+    const int nxt = cur ^ 1;
+    __syncthreads();
+    if (!take_all) {
+      for (int i = tid; i < radix_bins(level + 1); i += NT) s.hist[i] = 0u;
+      if (tid == 0) s.list_count[nxt] = 0u;
+    }
+    __syncthreads();
+    auto visit = [&](uint32_t k, uint32_t pos) {
+      const uint32_t d = radix_digit(level, k, pos);
+      if (d > tb || (take_all && d == tb)) atomicOr(&s.bitmap[pos >> 5], 1u << (pos & 31));
+      if (!take_all && d == tb) {
+        atomicAdd(&s.hist[radix_digit(level + 1, k, pos)], 1u);
+        if (collect) {
+          const uint32_t sl = atomicAdd(&s.list_count[nxt], 1u);
+          s.list_key[nxt][sl] = k;
+          s.list_pos[nxt][sl] = pos;
+        }
+      }
+    };
+    if (source_mode) {
+      for (int base = 0; base < len; base += 4 * NT) {
+        float x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = base + j * NT + tid;
+          x[j] = i < len ? row[i] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = base + j * NT + tid;
+          const uint32_t k = order_key(x[j]);
+          if (i < len && in_bucket(level, k, (uint32_t)i, thr)) visit(k, (uint32_t)i);
+        }
+      }
+    } else {
+      for (uint32_t e = tid; e < list_n; e += NT) visit(s.list_key[cur][e], s.list_pos[cur][e]);
+    }
+    __syncthreads();
+    if (take_all) break;
+    if (collect) {
+      source_mode = false;
+      cur = nxt;
+      list_n = s.list_count[cur];
+    }
+  }
+
+  // ---- 4. compaction in position order (two words per thread) and output
+  const int wpt = (nwords + NT - 1) / NT;
+  const int w_begin = min(tid * wpt, nwords), w_end = min(w_begin + wpt, nwords);
+  uint32_t cnt = 0;
+  for (int w = w_begin; w < w_end; ++w) cnt += __popc(s.bitmap[w]);
+  uint32_t total = 0;
+  uint32_t at = block_exclusive_scan<NT>(s.wave_sum, cnt, &total);
+  uint32_t* sel = s.list_pos[0];
+  __syncthreads();  // the list buffers are done with
+  for (int w = w_begin; w < w_end; ++w) {
+    uint32_t bits = s.bitmap[w];
+    while (bits) {
+      const int bit = __ffs(bits) - 1;
+      bits &= bits - 1;
+      if (at < (uint32_t)top_k) sel[at] = (uint32_t)((w << 5) + bit);
+      ++at;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < top_k; i += NT) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
+}
+
 __global__ void topk_to_physical_kernel(const int32_t* __restrict__ topk, int64_t topk_stride,
                                         const int32_t* __restrict__ bt, int64_t bt_stride,
                                         int table_width, int rows, int k, int rows_per_table,
@@ -492,6 +704,9 @@ static int prepare_topk_kernel() {
   if (status < 0) {
     hipError_t e = hipFuncSetAttribute((const void*)topk_finish_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTopkSmemBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)topk_onepass_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kTopkSmemBytes);
     status = e == hipSuccess ? 0 : 1;
     if (status) return set_error(kLaunchFailed, "topk: cannot reserve %zu B of LDS: %s",
                                  kTopkSmemBytes, hipGetErrorString(e));
@@ -505,6 +720,13 @@ static int launch_topk(const RowIn& in, int batch, const int32_t* offsets, const
                        int top_k, void* workspace, size_t workspace_bytes, hipStream_t stream,
                        const char* what) {
   if (int rc = prepare_topk_kernel()) return rc;
+  const bool aligned = (reinterpret_cast<uintptr_t>(in.scores) & 15) == 0 && (in.stride & 3) == 0 && !in.row_starts;
+  if (in.max_len <= kRegMaxLen && aligned) {
+    // the whole row fits in one workgroup's registers: one launch, no workspace
+    hipLaunchKernelGGL(topk_onepass_kernel, dim3(batch), dim3(kRegThreads), kTopkSmemBytes, stream, in, offsets,
+                       page_table, pt_stride, page_bits, out_page, out_raw, top_k);
+    return check_launch(what);
+  }
   RowWs* ws = nullptr;
   if (workspace) {
     if (workspace_bytes < (size_t)batch * sizeof(RowWs))

@@ -171,3 +171,25 @@ def test_rejects_bad_arguments(cuda):
         deepseek_v4.topk_transform(s, lens, pt, out, 48, 512)
     with pytest.raises(ValueError, match="ragged Indexer top_k must be 2048"):
         deepseek_v4.topk_transform_ragged(s, lens, lens, lens, out, 512)
+
+
+def test_sample_blind_spots_fall_back_exactly(cuda):
+    """Rows of up to 64K positions take the one-launch path, whose threshold comes
+    from a 1/8 sample of the row. Scores that put the whole top-k where the sample
+    does not look (positions 1 mod 4), or that make every position a candidate
+    (a constant row), must still give the exact answer through the fallback."""
+    L = 65536
+    rng = np.random.default_rng(7)
+    base = rng.standard_normal(L).astype(np.float32)
+    blind = base.copy()
+    blind[1::4] += 100.0                 # 16384 large scores, none sampled
+    const = np.full(L, 0.5, np.float32)  # every position ties
+    ramp = np.arange(L, dtype=np.float32)  # scores rise with position
+    scores = np.stack([blind, const, ramp, base])
+    lens = np.array([L, L, L, 40000], np.int32)
+    pt = np.stack([np.random.default_rng(i).permutation(L // 64).astype(np.int32) for i in range(4)])
+    out, raw = _run(torch.from_numpy(scores).to(cuda), torch.from_numpy(lens).to(cuda),
+                    torch.from_numpy(pt).to(cuda), 64, 2048)
+    e_page, e_raw = O.topk_transform(scores, lens, pt, 64, 2048)
+    assert np.array_equal(raw, e_raw)
+    assert np.array_equal(out, e_page)
