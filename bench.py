@@ -1,20 +1,23 @@
 """DSA decode step benchmark on one MI355X.
 
-One step = indexer logits (fp8 MFMA over the paged indexer cache) -> exact
-top-2048 with page translation -> sparse MLA decode over the paged fp8 MLA
-cache, for batch 128, next_n 1, 64K context per sequence, 64 indexer heads x
-128, 128 MLA heads x 576/512. Inputs are seeded synthetic data already resident
-in HBM; block tables are a random permutation of the page pool.
+One step = fp8 lightning indexer (fp8 MFMA over the paged indexer cache) ->
+exact top-2048 with page translation -> sparse MLA decode over the paged fp8
+MLA cache, for batch 128, next_n 1, 64K context per sequence, 64 indexer heads
+x 128, 128 MLA heads x 576/512. The indexer and the top-k run fused
+(dsa_indexer_topk: the logits never reach memory); --unfused runs them as two
+operators over a logits buffer instead. Inputs are seeded synthetic data
+already resident in HBM; block tables are a random permutation of the page pool.
 
 Prints ONE JSON line. `value` is decode tokens/s (= batch / step time);
-`roofline` covers the dominant kernel (the indexer, HBM-bound), measured with
-HIP events on the stream the kernels run on; `stages` reports every kernel;
-`cpu_baseline` times the numpy oracle of the same step on a bounded sample of
-the sequences on the host cores.
+`roofline` covers the dominant kernel (the indexer's filter pass over every key
+page, HBM-bound), timed with HIP events that the library records on the stream
+the kernels run on; `stages` reports every phase; `cpu_baseline` times the numpy
+oracle of the same step on a bounded sample of the sequences on the host cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--unfused]
        python bench.py --copy-calib   (a plain 1 GiB device copy, for scaling
                                        rocprofv3 FETCH_SIZE/WRITE_SIZE)
+       python bench.py --only {fused,indexer,topk,mla}   (profiling: one stage only)
 """
 from __future__ import annotations
 
@@ -32,7 +35,7 @@ METRIC = "DSA decode µs/step & tokens/s at B=128,64K ctx,k=2048; % HBM / fp8-MF
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "indexer_config2_pmc.txt")
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "indexer_filter_config2_pmc.txt")
 
 
 def parse_args():
@@ -48,13 +51,14 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample")
     p.add_argument("--copy-calib", action="store_true")
-    p.add_argument("--only", choices=["indexer", "topk", "mla"], default=None,
+    p.add_argument("--unfused", action="store_true", help="indexer logits + top-k as two operators")
+    p.add_argument("--only", choices=["fused", "indexer", "topk", "mla"], default=None,
                    help="profiling aid: launch only this stage in the timed loop (no JSON line)")
     return p.parse_args()
 
 
 def pmc_traffic():
-    """HBM bytes per indexer launch from the committed rocprofv3 PMC summary, if any."""
+    """HBM bytes per filter-kernel launch from the committed rocprofv3 PMC summary, if any."""
     try:
         with open(PMC_SUMMARY) as f:
             m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read(), re.M)
@@ -132,37 +136,53 @@ def main():
     q_mla = synth.make_mla_query(B, H, seed=args.seed, device=dev)
     scale = 192 ** -0.5
     max_ctx = inp.block_tables.shape[1] * 64
-    step = DsaDecodeStep(B, 1, max_ctx, num_heads=H, index_topk=K, device=dev)
+    step = DsaDecodeStep(B, 1, max_ctx, num_heads=H, index_topk=K, device=dev, fused=not args.unfused)
     seq = inp.context_lens
     bt = inp.block_tables
+    from nanoengine_amd import ops
     torch.cuda.synchronize()
 
     def run(ev=None):
-        from nanoengine_amd import ops
-        if ev is not None:
-            ev[0].record()
-        ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
-                           max_ctx, out=step.logits)
-        if ev is not None:
-            ev[1].record()
-        ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical, workspace=step.topk_workspace)
-        if ev is not None:
-            ev[2].record()
+        # ev: [start, after sample, after filter, after finish, after repair, after MLA]
+        if step.fused:
+            ops.indexer_topk(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt, max_ctx, K,
+                             step.physical, step.logical, workspace=step.fused_workspace,
+                             phase_events=ev[0:5] if ev is not None else None)
+        else:
+            if ev is not None:
+                ev[0].record()
+            ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+                               max_ctx, out=step.logits)
+            if ev is not None:
+                ev[1].record()
+                ev[2].record()
+            ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical,
+                               workspace=step.topk_workspace)
+            if ev is not None:
+                ev[3].record()
+                ev[4].record()
         ops.sparse_mla_decode(q_mla, kv, step.physical, scale, out=step.out, lse=step.lse,
                               num_splits=step.num_splits, workspace=step.workspace)
         if ev is not None:
-            ev[3].record()
+            ev[5].record()
 
     if args.only:
-        from nanoengine_amd import ops
         run()
         torch.cuda.synchronize()
+        logits = torch.empty(B, max_ctx, dtype=torch.float32, device=dev) if args.only in ("indexer", "topk") else None
+        if logits is not None:
+            ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+                               max_ctx, out=logits)
         for _ in range(args.steps):
-            if args.only == "indexer":
+            if args.only == "fused":
+                ops.indexer_topk(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+                                 max_ctx, K, step.physical, step.logical,
+                                 workspace=getattr(step, "fused_workspace", None))
+            elif args.only == "indexer":
                 ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
-                                   max_ctx, out=step.logits)
+                                   max_ctx, out=logits)
             elif args.only == "topk":
-                ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical, workspace=step.topk_workspace)
+                ops.topk_transform(logits, seq, bt, step.physical, 64, K, step.logical)
             else:
                 ops.sparse_mla_decode(q_mla, kv, step.physical, scale, out=step.out, lse=step.lse,
                                       num_splits=step.num_splits, workspace=step.workspace)
@@ -181,19 +201,22 @@ def main():
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
 
-    # per-stage durations with HIP events on the launch stream (separate pass)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    # per-phase durations with HIP events on the launch stream (separate pass)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
     for e in evs:
         run(e)
     torch.cuda.synchronize()
-    st = [[e[i].elapsed_time(e[i + 1]) * 1e3 for e in evs] for i in range(3)]   # us
-    med = [sorted(x)[len(x) // 2] for x in st]
-    avg = [sum(x) / len(x) for x in st]
+    ph = [[e[i].elapsed_time(e[i + 1]) * 1e3 for e in evs] for i in range(5)]   # us
+    med = [sorted(x)[len(x) // 2] for x in ph]
+    avg = [sum(x) / len(x) for x in ph]
+    idx_total = sum(avg[0:4])
 
     total_tokens = sum(lens)
-    idx_bytes = total_tokens * 132 + B * 64 * 128 + B * 64 * 4 + B * max_ctx * 4
+    # the filter pass reads every key page of every sequence (+ q and head weights)
+    idx_bytes = total_tokens * 132 + B * 64 * 128 + B * 64 * 4
+    if not step.fused:
+        idx_bytes += B * max_ctx * 4  # the logits written
     idx_flops = 2.0 * 64 * 128 * total_tokens
-    topk_bytes = B * max_ctx * 4 * 2 + B * K * 4 * 2 + B * (max_ctx // 64) * 4
     valid = int((step.physical >= 0).sum().item())
     mla_bytes = valid * 656 + B * H * 576 * 2 + B * H * 512 * 2 + B * H * 4 + B * K * 4
     mla_flops = 2.0 * H * (576 + 512) * valid
@@ -201,25 +224,33 @@ def main():
     def gbs(b, us):
         return b / (us * 1e-6) / 1e9
 
+    r4 = lambda x: round(x, 4)
     stages = {
-        "indexer_logits": {"us": round(avg[0], 2), "us_median": round(med[0], 2), "bytes": idx_bytes,
-                           "GBps": round(gbs(idx_bytes, avg[0]), 1),
-                           "hbm_frac": round(gbs(idx_bytes, avg[0]) / HBM_PEAK_GBS, 4),
-                           "fp8_mfma_frac": round(idx_flops / (avg[0] * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4)},
-        "topk_transform": {"us": round(avg[1], 2), "us_median": round(med[1], 2), "bytes": topk_bytes,
-                           "GBps": round(gbs(topk_bytes, avg[1]), 1),
-                           "hbm_frac": round(gbs(topk_bytes, avg[1]) / HBM_PEAK_GBS, 4)},
-        "sparse_mla_decode": {"us": round(avg[2], 2), "us_median": round(med[2], 2), "bytes": mla_bytes,
-                              "GBps": round(gbs(mla_bytes, avg[2]), 1),
-                              "hbm_frac": round(gbs(mla_bytes, avg[2]) / HBM_PEAK_GBS, 4),
-                              "bf16_mfma_frac": round(mla_flops / (avg[2] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "indexer_topk": {
+            "us": round(idx_total, 2), "fused": step.fused,
+            "phases_us": {"sample+threshold": round(avg[0], 2), "filter": round(avg[1], 2),
+                          "finish": round(avg[2], 2), "repair": round(avg[3], 2)},
+            "filter_bytes": idx_bytes, "filter_GBps": round(gbs(idx_bytes, avg[1]), 1),
+            "filter_hbm_frac": r4(gbs(idx_bytes, avg[1]) / HBM_PEAK_GBS),
+            "filter_fp8_mfma_frac": r4(idx_flops / (avg[1] * 1e-6) / 1e12 / FP8_PEAK_TFLOPS)},
+        "sparse_mla_decode": {"us": round(avg[4], 2), "us_median": round(med[4], 2), "bytes": mla_bytes,
+                              "GBps": round(gbs(mla_bytes, avg[4]), 1),
+                              "hbm_frac": r4(gbs(mla_bytes, avg[4]) / HBM_PEAK_GBS),
+                              "bf16_mfma_frac": r4(mla_flops / (avg[4] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS),
                               "num_splits": step.num_splits},
     }
-    achieved = gbs(idx_bytes, avg[0])
+    if not step.fused:
+        stages["indexer_topk"] = {"us": round(idx_total, 2), "fused": False,
+                                  "phases_us": {"indexer_logits": round(avg[0] + avg[1], 2),
+                                                "topk_transform": round(avg[2] + avg[3], 2)},
+                                  "indexer_bytes": idx_bytes,
+                                  "indexer_GBps": round(gbs(idx_bytes, avg[0] + avg[1]), 1)}
+    filt_us = avg[1] if step.fused else avg[0] + avg[1]
+    achieved = gbs(idx_bytes, filt_us)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
-                "kernel": "indexer_logits_kernel<1>", "bytes_per_launch": idx_bytes,
-                "avg_launch_us": round(avg[0], 2)}
+                "frac": r4(achieved / HBM_PEAK_GBS), "traffic": pmc_traffic() if step.fused else None,
+                "kernel": "indexer_logits_kernel<1, kIdxFilter>" if step.fused else "indexer_logits_kernel<1, kIdxStore>",
+                "bytes_per_launch": idx_bytes, "avg_launch_us": round(filt_us, 2)}
 
     cpu = None
     if not args.no_cpu_baseline:

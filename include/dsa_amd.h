@@ -79,6 +79,37 @@ DSA_API int dsa_indexer_logits(const uint8_t* q_fp8, const uint8_t* kv_cache,
                        int page_size, int64_t max_context_len,
                        float* logits, int64_t logits_stride, void* stream);
 
+/* Workspace bytes dsa_indexer_topk needs for this shape. */
+DSA_API size_t dsa_indexer_topk_workspace_bytes(int batch, int next_n, int64_t max_context_len);
+
+/* Fused decode indexer + exact top-k + page translation, without materialising
+ * the logits. Inputs as dsa_indexer_logits; outputs as dsa_topk_transform:
+ *   out_physical [batch*next_n, top_k] int32 cache slots
+ *                block_tables[row / next_n, pos / 64] * 64 + pos % 64, -1 padded
+ *   out_logical  [batch*next_n, top_k] int32 token positions (may be NULL)
+ * Selection, order (ascending position), ties (lowest positions) and padding are
+ * those of dsa_topk_transform over dsa_indexer_logits' logits, exactly.
+ * Launch sequence on `stream`: logits of every 32nd page -> per-row score
+ * threshold -> all pages, keeping only (key, position) of tokens at or above the
+ * threshold in per-row lists -> exact top-k of each list; a row whose list is
+ * unusable (fewer than top_k or more than the list capacity) is redone from its
+ * full logits by two more launches that return at once for every other row.
+ * phase_events: NULL, or five hipEvent_t (entries may be NULL) recorded on
+ * `stream` before the first launch and after the sample, filter, finish and
+ * repair phases, for timing.
+ * top_k in {512, 2048}; rows of at most dsa_topk_max_len() positions. The
+ * workspace (dsa_indexer_topk_workspace_bytes) should be zero-filled before its
+ * first use; a stale one gives the same results, its first call more slowly.
+ * Replaces the kernel sequence of Indexer.forward(..., translate_topk=True)
+ * (deep_gemm.fp8_paged_mqa_logits then topk_transform, lightning.py:1395-1466;
+ * chosen by _can_use_fused_indexer_topk, deepseek_v2.py:78-81, 1917-1935). */
+DSA_API int dsa_indexer_topk(const uint8_t* q_fp8, const uint8_t* kv_cache, const float* weights,
+                             const int32_t* context_lens, const int32_t* block_tables,
+                             int64_t block_table_stride, int batch, int next_n, int num_heads,
+                             int head_dim, int page_size, int64_t max_context_len, int top_k,
+                             int32_t* out_physical, int32_t* out_logical, void* workspace,
+                             size_t workspace_bytes, void* stream, void* const* phase_events);
+
 /* Workspace bytes the top-k entry points use for `batch` rows (per-row
  * threshold, counter and a 4096-entry candidate list: 32 KB + 16 B a row). */
 DSA_API size_t dsa_topk_workspace_bytes(int batch);

@@ -21,6 +21,9 @@ SIGNATURES = {
     "dsa_indexer_schedule": (c_int, [_P, c_int, c_int, c_int, _P, _P]),
     "dsa_indexer_logits": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, c_int,
                                    c_int64, _P, c_int64, _P]),
+    "dsa_indexer_topk_workspace_bytes": (c_size_t, [c_int, c_int, c_int64]),
+    "dsa_indexer_topk": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, c_int, c_int64, c_int,
+                                 _P, _P, _P, c_size_t, _P, _P]),
     "dsa_topk_workspace_bytes": (c_size_t, [c_int]),
     "dsa_topk_transform": (c_int, [_P, c_int64, _P, _P, c_int64, _P, _P, c_int, c_int64, c_int, c_int, _P,
                                    c_size_t, _P]),

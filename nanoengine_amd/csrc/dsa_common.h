@@ -69,9 +69,67 @@ __device__ __forceinline__ void dequant16_fp8_bf16(v4i raw, float scale, v4i& lo
   }
 }
 
+// Per-row candidate list of the exact top-k (device workspace): a score
+// threshold t_key (order key), the number of candidates appended, a flag set
+// when the list could not be used (fused indexer path), then the (key,
+// position) pairs. Filled by the top-k gather kernel or by the fused indexer.
+constexpr int kListCap = 6144;
+struct RowWs {
+  uint32_t t_key;
+  uint32_t count;
+  uint32_t failed;
+  uint32_t pad;
+  uint32_t key[kListCap];
+  uint32_t pos[kListCap];
+};
+
+// Launcher of the top-k finish for the fused indexer + top-k entry point (topk.hip).
+int launch_finish_fused(const float* logits, int64_t logits_stride, const int32_t* seq_lens, int64_t max_len,
+                        RowWs* ws, const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                        int32_t* out_page, int32_t* out_raw, int top_k, int rows, bool repair, hipStream_t stream);
+
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, 64);
+}
+
+// Block-wide (NT threads): find the bin tb with S(tb+1) < remain <= S(tb),
+// S(b) = sum of hist[b..nbins). Leaves tb, above = S(tb+1), eq = hist[tb] in
+// the shared *tb_out, *above_out, *eq_out for every thread after the call.
+template <int NT>
+__device__ void find_threshold(const uint32_t* hist, uint32_t* wave_sum, int nbins, uint32_t remain,
+                               uint32_t* tb_out, uint32_t* above_out, uint32_t* eq_out) {
+  constexpr int kWaves = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = nbins >= NT ? nbins / NT : 1;
+  const int first = tid * per;
+  uint32_t local = 0;
+  if (first < nbins)
+    for (int i = 0; i < per; ++i) local += hist[first + i];
+  // inclusive suffix sum inside the wave
+  uint32_t v = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    uint32_t n = __shfl_down(v, off, 64);
+    if (lane + off < 64) v += n;
+  }
+  if (lane == 0) wave_sum[wave] = v;
+  __syncthreads();
+  uint32_t higher = v - local;
+  for (int w = wave + 1; w < kWaves; ++w) higher += wave_sum[w];
+  if (first < nbins) {
+    uint32_t acc = higher;
+    for (int i = per - 1; i >= 0; --i) {
+      uint32_t h = hist[first + i];
+      if (acc < remain && acc + h >= remain) {
+        *tb_out = first + i;
+        *above_out = acc;
+        *eq_out = h;
+      }
+      acc += h;
+    }
+  }
+  __syncthreads();
 }
 
 }  // namespace dsa

@@ -32,7 +32,6 @@ namespace dsa {
 constexpr int kTopkThreads = 512;
 constexpr int kTopkMaxLen = 1 << 18;            // positions per row
 constexpr int kBitmapWords = kTopkMaxLen / 32;  // 32 KB of LDS
-constexpr int kListCap = 4096;                  // candidates per list buffer
 constexpr int kHistBins = 4096;
 constexpr uint32_t kIdxMax = (1u << 18) - 1;
 constexpr int kLevels = 5;
@@ -44,15 +43,6 @@ constexpr int kSampleEvery = 8;                 // one chunk in eight
 constexpr int kGatherPerThread = 32;
 constexpr int kGatherSpan = kAuxThreads * kGatherPerThread;  // 8192 positions per workgroup
 constexpr int kGatherLdsCap = 2048;             // candidates one gather workgroup can stage
-
-// Per-row workspace: header [t_key, count, pad, pad] then the candidate list.
-struct RowWs {
-  uint32_t t_key;
-  uint32_t count;
-  uint32_t pad[2];
-  uint32_t key[kListCap];
-  uint32_t pos[kListCap];
-};
 
 struct TopkSmem {
   uint32_t hist[kHistBins];
@@ -96,45 +86,6 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
 }
 
-// Block-wide (NT threads): find the bin tb with S(tb+1) < remain <= S(tb),
-// S(b) = sum of hist[b..nbins). Leaves tb, above = S(tb+1), eq = hist[tb] in
-// the shared *tb_out, *above_out, *eq_out for every thread after the call.
-template <int NT>
-__device__ void find_threshold(const uint32_t* hist, uint32_t* wave_sum, int nbins, uint32_t remain,
-                               uint32_t* tb_out, uint32_t* above_out, uint32_t* eq_out) {
-  constexpr int kWaves = NT / 64;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int per = nbins >= NT ? nbins / NT : 1;
-  const int first = tid * per;
-  uint32_t local = 0;
-  if (first < nbins)
-    for (int i = 0; i < per; ++i) local += hist[first + i];
-  // inclusive suffix sum inside the wave
-  uint32_t v = local;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    uint32_t n = __shfl_down(v, off, 64);
-    if (lane + off < 64) v += n;
-  }
-  if (lane == 0) wave_sum[wave] = v;
-  __syncthreads();
-  uint32_t higher = v - local;
-  for (int w = wave + 1; w < kWaves; ++w) higher += wave_sum[w];
-  if (first < nbins) {
-    uint32_t acc = higher;
-    for (int i = per - 1; i >= 0; --i) {
-      uint32_t h = hist[first + i];
-      if (acc < remain && acc + h >= remain) {
-        *tb_out = first + i;
-        *above_out = acc;
-        *eq_out = h;
-      }
-      acc += h;
-    }
-  }
-  __syncthreads();
-}
-
 // Exclusive block prefix sum of one value per thread; returns the prefix and
 // writes the block total to *total (all threads).
 template <int NT>
@@ -159,6 +110,13 @@ __device__ uint32_t block_exclusive_scan(uint32_t* wave_sum, uint32_t x, uint32_
   *total = all;
   return before + v - x;
 }
+
+// topk_finish_kernel modes
+enum FinishMode : int {
+  kFinishNormal = 0,    // list if usable, else the full select over the row
+  kFinishListOnly = 1,  // list if usable, else flag the row (fused indexer: no logits yet)
+  kFinishRepair = 2,    // flagged rows only, full select over their (recomputed) logits
+};
 
 struct RowOut {
   int32_t* page;       // page-translated output (or the untranslated output)
@@ -206,7 +164,7 @@ topk_threshold_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
   const int len = in.len(b);
   RowWs& w = ws[b];
   if (len <= top_k) {
-    if (tid == 0) { w.t_key = 0u; w.count = 0u; }
+    if (tid == 0) { w.t_key = 0u; w.count = 0u; w.failed = 0u; }
     return;
   }
   const float* row = in.row(b);
@@ -260,6 +218,7 @@ topk_threshold_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
   if (tid == 0) {
     w.t_key = t_key;
     w.count = 0u;
+    w.failed = 0u;
   }
 }
 
@@ -326,20 +285,22 @@ topk_gather_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
 
 // ---------------------------------------------------------------- 3. finish
 __global__ void __launch_bounds__(kTopkThreads)
-topk_finish_kernel(const RowIn in, const RowWs* __restrict__ ws, const int32_t* __restrict__ offsets,
-                   const int32_t* __restrict__ page_table, int64_t pt_stride, uint32_t page_bits,
-                   int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k) {
+topk_finish_kernel(const RowIn in, RowWs* __restrict__ ws, const int32_t* __restrict__ offsets,
+                   const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                   int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k, int mode) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   TopkSmem& s = *reinterpret_cast<TopkSmem*>(smem_raw);
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
   const int len = in.len(b);
   const float* row = in.row(b);
+  // kFinishRepair: only rows whose list was unusable, from their logits
+  if (mode == kFinishRepair && !ws[b].failed) return;
 
   RowOut out;
   out.page = out_page + (int64_t)b * top_k;
   out.raw = out_raw ? out_raw + (int64_t)b * top_k : nullptr;
-  out.pt = page_table ? page_table + (int64_t)b * pt_stride : nullptr;
+  out.pt = page_table ? page_table + (int64_t)(b / pt_div) * pt_stride : nullptr;
   out.page_bits = page_bits;
   out.offset = offsets ? offsets[b] : 0;
 
@@ -353,7 +314,12 @@ topk_finish_kernel(const RowIn in, const RowWs* __restrict__ ws, const int32_t* 
   for (int i = tid; i < kHistBins; i += kTopkThreads) s.hist[i] = 0u;
   if (tid < 2) s.list_count[tid] = 0u;
   const uint32_t cand = ws ? ws[b].count : 0u;
-  const bool listed = ws && cand >= (uint32_t)top_k && cand <= (uint32_t)kListCap;
+  const bool listed = ws && mode != kFinishRepair && cand >= (uint32_t)top_k && cand <= (uint32_t)kListCap;
+  if (mode == kFinishListOnly && !listed) {
+    // no logits to fall back on: flag the row for the repair launches
+    if (tid == 0) ws[b].failed = 1u;
+    return;
+  }
   __syncthreads();
 
   uint32_t thr[kLevels] = {0, 0, 0, 0, 0};
@@ -742,8 +708,19 @@ static int launch_topk(const RowIn& in, int batch, const int32_t* offsets, const
                          top_k, ws);
   }
   hipLaunchKernelGGL(topk_finish_kernel, dim3(batch), dim3(kTopkThreads), kTopkSmemBytes, stream, in, ws,
-                     offsets, page_table, pt_stride, page_bits, out_page, out_raw, top_k);
+                     offsets, page_table, pt_stride, 1, page_bits, out_page, out_raw, top_k, (int)kFinishNormal);
   return check_launch(what);
+}
+
+int launch_finish_fused(const float* logits, int64_t logits_stride, const int32_t* seq_lens, int64_t max_len,
+                        RowWs* ws, const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                        int32_t* out_page, int32_t* out_raw, int top_k, int rows, bool repair, hipStream_t stream) {
+  if (int rc = prepare_topk_kernel()) return rc;
+  const RowIn in{logits, logits_stride, seq_lens, nullptr, max_len};
+  hipLaunchKernelGGL(topk_finish_kernel, dim3(rows), dim3(kTopkThreads), kTopkSmemBytes, stream, in, ws, nullptr,
+                     page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k,
+                     (int)(repair ? kFinishRepair : kFinishListOnly));
+  return check_launch("dsa_indexer_topk(finish)");
 }
 
 }  // namespace dsa

@@ -105,6 +105,69 @@ def indexer_logits(q_fp8: torch.Tensor, kv_cache: torch.Tensor, weights: torch.T
     return out
 
 
+def indexer_topk_workspace_bytes(batch: int, next_n: int, max_context_len: int) -> int:
+    return int(_lib.load().dsa_indexer_topk_workspace_bytes(batch, next_n, int(max_context_len)))
+
+
+def indexer_topk(q_fp8: torch.Tensor, kv_cache: torch.Tensor, weights: torch.Tensor,
+                 context_lens: torch.Tensor, block_tables: torch.Tensor, max_context_len: int, top_k: int,
+                 out_physical: torch.Tensor, out_logical: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None,
+                 phase_events: list | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Fused indexer + exact top-k + page translation (see dsa_indexer_topk):
+    the same result as topk_transform over indexer_logits, without the logits.
+    ``phase_events``: optional five torch.cuda.Event recorded before the first
+    launch and after the sample, filter, finish and repair phases (on the
+    current stream)."""
+    _require(q_fp8.dim() == 4, f"q_fp8 must be [B, next_n, H, D], got {tuple(q_fp8.shape)}")
+    B, n, H, D = q_fp8.shape
+    _require(q_fp8.dtype in (torch.float8_e4m3fn, torch.uint8) and q_fp8.is_contiguous(), "q_fp8 fp8 contiguous")
+    _require(kv_cache.dtype in (torch.uint8, torch.float8_e4m3fn) and kv_cache.is_contiguous(), "kv_cache bytes")
+    num_pages = kv_cache.shape[0]
+    page_bytes = kv_cache.numel() // max(num_pages, 1)
+    _require(page_bytes % (D + 4) == 0, f"kv_cache page of {page_bytes} B is not page_size*{D + 4}")
+    page_size = page_bytes // (D + 4)
+    _require(weights.dtype == torch.float32 and tuple(weights.shape) == (B * n, H), "weights must be f32 [B*n, H]")
+    weights = weights.contiguous()
+    cl = context_lens.reshape(B, -1)
+    _require(cl.shape[1] == n, f"context_lens must be [B, next_n]={B, n}, got {tuple(context_lens.shape)}")
+    cl = cl.to(torch.int32).contiguous()
+    _require(block_tables.dim() == 2 and block_tables.shape[0] == B, "block_tables must be [B, M]")
+    bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
+    _require(bt.stride(1) == 1, "block_tables rows must be contiguous")
+    _require(bt.shape[1] * page_size >= max_context_len, "block_tables too narrow for max_context_len")
+    for o in (out_physical, out_logical):
+        if o is not None:
+            _require(o.dtype == torch.int32 and tuple(o.shape) == (B * n, top_k) and o.is_contiguous(),
+                     f"outputs must be int32 [{B * n}, {top_k}] contiguous")
+    dev = _check_cuda(q_fp8, kv_cache, weights, cl, bt, out_physical)
+    need = indexer_topk_workspace_bytes(B, n, max_context_len)
+    if workspace is None:
+        workspace = torch.zeros(need, dtype=torch.uint8, device=dev)
+    _require(workspace.dtype == torch.uint8 and workspace.numel() >= need, f"workspace needs {need} bytes")
+    _lib.call("dsa_indexer_topk", _as_bytes(q_fp8).data_ptr(), _as_bytes(kv_cache).data_ptr(),
+              weights.data_ptr(), cl.data_ptr(), bt.data_ptr(), bt.stride(0), B, n, H, D, page_size,
+              int(max_context_len), int(top_k), out_physical.data_ptr(),
+              out_logical.data_ptr() if out_logical is not None else None, workspace.data_ptr(),
+              workspace.numel(), _stream(dev), _event_array(phase_events))
+    return out_physical, out_logical
+
+
+def _event_array(events):
+    if not events:
+        return None
+    import ctypes
+    handles = []
+    for e in events:
+        if e is None:
+            handles.append(None)
+        else:
+            if e.cuda_event == 0:  # torch creates the HIP event lazily
+                e.record()
+            handles.append(e.cuda_event)
+    return (ctypes.c_void_p * len(handles))(*handles)
+
+
 # --------------------------------------------------------------------------- top-k
 _TOPK_WS: dict = {}
 

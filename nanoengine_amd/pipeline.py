@@ -5,8 +5,10 @@ This is the composition ``DeepseekV2Attention.forward`` performs per layer in
 decode (dlengine/runtime/models/deepseek_v2/deepseek_v2.py:1860-2018 calling
 ``Indexer.forward`` lightning.py:1357-1466 with ``translate_topk=True`` and then
 ``FlashMlaAttention.forward`` flash_mla.py:76-99). Every buffer is allocated
-once in the constructor, so a step is three kernel launches and no allocation
-(capturable in a HIP graph).
+once in the constructor, so a step allocates nothing (capturable in a HIP
+graph). By default the indexer and the top-k run fused (``ops.indexer_topk``:
+the logits are never written to memory); ``fused=False`` runs them as the two
+separate reference operators over a logits buffer.
 """
 from __future__ import annotations
 
@@ -17,12 +19,18 @@ from . import ops
 
 class DsaDecodeStep:
     def __init__(self, batch: int, next_n: int, max_context_len: int, num_heads: int = 128,
-                 index_topk: int = 2048, page_size: int = 64, device="cuda"):
+                 index_topk: int = 2048, page_size: int = 64, device="cuda", fused: bool = True):
         self.batch, self.next_n, self.max_ctx = batch, next_n, max_context_len
         self.num_heads, self.topk, self.page_size = num_heads, index_topk, page_size
+        self.fused = fused
         rows = batch * next_n
         dev = torch.device(device)
-        self.logits = torch.empty(rows, max_context_len, dtype=torch.float32, device=dev)
+        if fused:
+            self.logits = None
+            self.fused_workspace = torch.zeros(ops.indexer_topk_workspace_bytes(batch, next_n, max_context_len),
+                                               dtype=torch.uint8, device=dev)
+        else:
+            self.logits = torch.empty(rows, max_context_len, dtype=torch.float32, device=dev)
         self.logical = torch.empty(rows, index_topk, dtype=torch.int32, device=dev)
         self.physical = torch.empty(rows, index_topk, dtype=torch.int32, device=dev)
         self.out = torch.empty(rows, num_heads, ops.MLA_D_V, dtype=torch.bfloat16, device=dev)
@@ -49,10 +57,15 @@ class DsaDecodeStep:
         repeated per query token); q_mla [B*n, H, 576] bf16; kv_cache
         [blocks, 64, 1, 656] fp8 bytes. Returns (o, lse, logical, physical)."""
         B, n = self.batch, self.next_n
-        ops.indexer_logits(q_idx_fp8.view(B, n, *q_idx_fp8.shape[1:]), indexer_cache, weights,
-                           seq_lens.view(B, n), block_tables, self.max_ctx, out=self.logits)
-        ops.topk_transform(self.logits, seq_lens, page_tables, self.physical, self.page_size, self.topk,
-                           self.logical, workspace=self.topk_workspace)
+        q4 = q_idx_fp8.view(B, n, *q_idx_fp8.shape[1:])
+        if self.fused:
+            ops.indexer_topk(q4, indexer_cache, weights, seq_lens.view(B, n), block_tables, self.max_ctx,
+                             self.topk, self.physical, self.logical, workspace=self.fused_workspace)
+        else:
+            ops.indexer_logits(q4, indexer_cache, weights, seq_lens.view(B, n), block_tables, self.max_ctx,
+                               out=self.logits)
+            ops.topk_transform(self.logits, seq_lens, page_tables, self.physical, self.page_size, self.topk,
+                               self.logical, workspace=self.topk_workspace)
         ops.sparse_mla_decode(q_mla, kv_cache, self.physical, sm_scale, out=self.out, lse=self.lse,
                               num_splits=self.num_splits, workspace=self.workspace)
         return self.out, self.lse, self.logical, self.physical
