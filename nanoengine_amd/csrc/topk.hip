@@ -646,6 +646,134 @@ topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const i
   for (int i = tid; i < top_k; i += NT) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
 }
 
+// ---------------------------------------------------------------- list select
+// Exact top-k of a row's candidate list (fused indexer path): every candidate
+// has key >= t_key, so the radix runs over the 50-bit composite
+//   [ key - t_key : nb bits ][ (2^18-1) - position : 18 bits ]
+// where nb = bit length of (max key - t_key), in 12-bit digits from the top:
+// the digits spread over the candidates' actual range instead of the fixed
+// bit positions of the full select, where most candidates share the top
+// digits. A row whose list is unusable (fewer than k or more than the list
+// capacity) is flagged for the repair launches.
+__global__ void __launch_bounds__(kTopkThreads)
+topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* __restrict__ ws,
+                 const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                 int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  TopkSmem& s = *reinterpret_cast<TopkSmem*>(smem_raw);
+  constexpr int NT = kTopkThreads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x;
+  const int64_t l = seq_lens[b];
+  const int len = (int)(l < 0 ? 0 : (l > max_len ? max_len : l));
+  RowWs& w = ws[b];
+
+  RowOut out;
+  out.page = out_page + (int64_t)b * top_k;
+  out.raw = out_raw ? out_raw + (int64_t)b * top_k : nullptr;
+  out.pt = page_table ? page_table + (int64_t)(b / pt_div) * pt_stride : nullptr;
+  out.page_bits = page_bits;
+  out.offset = 0;
+
+  if (len <= top_k) {
+    for (int i = tid; i < top_k; i += NT) out.emit(i, i < len ? i : -1);
+    return;
+  }
+  const uint32_t cand = w.count;
+  if (cand < (uint32_t)top_k || cand > (uint32_t)kListCap) {
+    if (tid == 0) w.failed = 1u;
+    return;
+  }
+  const uint32_t t_key = w.t_key;
+
+  // candidates into LDS as composite (hi = key - t_key, lo = inverted position), and their max
+  uint32_t* hi = s.list_key[0];
+  uint32_t* lo = s.list_pos[0];
+  uint32_t mx = 0;
+  for (uint32_t e = tid; e < cand; e += NT) {
+    const uint32_t rk = w.key[e] - t_key;
+    hi[e] = rk;
+    lo[e] = kIdxMax - w.pos[e];
+    mx = max(mx, rk);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor(mx, off, 64));
+  if (lane == 0) s.wave_sum[wave] = mx;
+  const int nwords = (len + 31) >> 5;
+  for (int i = tid; i < nwords; i += NT) s.bitmap[i] = 0u;
+  __syncthreads();
+  mx = 0;
+  for (int i = 0; i < NT / 64; ++i) mx = max(mx, s.wave_sum[i]);
+  const int nb = 32 - __clz(mx);            // bits of the key part (0: all equal)
+  const int total_bits = nb + 18;
+  const int nlev = (total_bits + 11) / 12;
+  auto composite = [&](uint32_t h, uint32_t p) { return ((uint64_t)h << 18) | p; };
+  // digit of level L: bits [total - 12(L+1), total - 12L) of the composite
+  auto digit = [&](uint64_t c, int L) {
+    const int top = total_bits - 12 * L;
+    const int lo_b = max(top - 12, 0);
+    return (uint32_t)((c >> lo_b) & ((1ull << (top - lo_b)) - 1ull));
+  };
+
+  uint32_t remain = (uint32_t)top_k;
+  int cur = 0;
+  uint32_t n = cand;
+  __syncthreads();
+  for (int L = 0; L < nlev; ++L) {
+    const int top = total_bits - 12 * L;
+    const int lo_b = max(top - 12, 0);
+    const int nbins = 1 << (top - lo_b);
+    for (int i = tid; i < nbins; i += NT) s.hist[i] = 0u;
+    if (tid < 2) s.list_count[tid] = 0u;
+    __syncthreads();
+    for (uint32_t e = tid; e < n; e += NT)
+      atomicAdd(&s.hist[digit(composite(s.list_key[cur][e], s.list_pos[cur][e]), L)], 1u);
+    __syncthreads();
+    find_threshold<NT>(s.hist, s.wave_sum, nbins, remain, &s.tb, &s.above, &s.eq);
+    const uint32_t tb = s.tb, above = s.above, eq = s.eq;
+    remain -= above;
+    const bool last = (eq == remain) || L == nlev - 1;
+    const int nxt = cur ^ 1;
+    for (uint32_t e = tid; e < n; e += NT) {
+      const uint32_t h = s.list_key[cur][e], p = s.list_pos[cur][e];
+      const uint32_t d = digit(composite(h, p), L);
+      if (d > tb || (last && d == tb)) {
+        const uint32_t pos = kIdxMax - p;
+        atomicOr(&s.bitmap[pos >> 5], 1u << (pos & 31));
+      } else if (!last && d == tb) {
+        const uint32_t slot = atomicAdd(&s.list_count[nxt], 1u);
+        s.list_key[nxt][slot] = h;
+        s.list_pos[nxt][slot] = p;
+      }
+    }
+    __syncthreads();
+    if (last) break;
+    n = s.list_count[nxt];
+    cur = nxt;
+  }
+
+  // compaction in position order and output
+  const int wpt = (nwords + NT - 1) / NT;
+  const int w_begin = min(tid * wpt, nwords), w_end = min(w_begin + wpt, nwords);
+  uint32_t cnt = 0;
+  for (int wd = w_begin; wd < w_end; ++wd) cnt += __popc(s.bitmap[wd]);
+  uint32_t total = 0;
+  uint32_t at = block_exclusive_scan<NT>(s.wave_sum, cnt, &total);
+  uint32_t* sel = s.hist;  // 4096 entries >= top_k
+  __syncthreads();
+  for (int wd = w_begin; wd < w_end; ++wd) {
+    uint32_t bits = s.bitmap[wd];
+    while (bits) {
+      const int bit = __ffs(bits) - 1;
+      bits &= bits - 1;
+      if (at < (uint32_t)top_k) sel[at] = (uint32_t)((wd << 5) + bit);
+      ++at;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < top_k; i += NT) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
+}
+
 __global__ void topk_to_physical_kernel(const int32_t* __restrict__ topk, int64_t topk_stride,
                                         const int32_t* __restrict__ bt, int64_t bt_stride,
                                         int table_width, int rows, int k, int rows_per_table,
@@ -672,6 +800,9 @@ static int prepare_topk_kernel() {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTopkSmemBytes);
     if (e == hipSuccess)
       e = hipFuncSetAttribute((const void*)topk_onepass_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kTopkSmemBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)topk_list_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)kTopkSmemBytes);
     status = e == hipSuccess ? 0 : 1;
     if (status) return set_error(kLaunchFailed, "topk: cannot reserve %zu B of LDS: %s",
@@ -716,11 +847,15 @@ int launch_finish_fused(const float* logits, int64_t logits_stride, const int32_
                         RowWs* ws, const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
                         int32_t* out_page, int32_t* out_raw, int top_k, int rows, bool repair, hipStream_t stream) {
   if (int rc = prepare_topk_kernel()) return rc;
+  if (!repair) {
+    hipLaunchKernelGGL(topk_list_kernel, dim3(rows), dim3(kTopkThreads), kTopkSmemBytes, stream, seq_lens, max_len,
+                       ws, page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k);
+    return check_launch("dsa_indexer_topk(select)");
+  }
   const RowIn in{logits, logits_stride, seq_lens, nullptr, max_len};
   hipLaunchKernelGGL(topk_finish_kernel, dim3(rows), dim3(kTopkThreads), kTopkSmemBytes, stream, in, ws, nullptr,
-                     page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k,
-                     (int)(repair ? kFinishRepair : kFinishListOnly));
-  return check_launch("dsa_indexer_topk(finish)");
+                     page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k, (int)kFinishRepair);
+  return check_launch("dsa_indexer_topk(repair select)");
 }
 
 }  // namespace dsa
