@@ -52,6 +52,9 @@ def parse_args():
     p.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample")
     p.add_argument("--copy-calib", action="store_true")
     p.add_argument("--unfused", action="store_true", help="indexer logits + top-k as two operators")
+    p.add_argument("--config", type=int, choices=[2, 3], default=2,
+                   help="2: decode B=128 x 64K (the headline); 3: MTP verify, B=64, next_n=2, "
+                        "lognormal lengths (median 16K, clipped to 2K-128K)")
     p.add_argument("--only", choices=["fused", "indexer", "topk", "mla"], default=None,
                    help="profiling aid: launch only this stage in the timed loop (no JSON line)")
     return p.parse_args()
@@ -129,34 +132,43 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     B, L, H, K = args.batch, args.ctx, args.heads, args.topk
-    lens = [L] * B
-    inp = synth.make_indexer_inputs(lens, next_n=1, seed=args.seed, device=dev)
+    n = 1
+    if args.config == 3:
+        import numpy as np
+        B, n = 64, 2
+        rng = np.random.default_rng(args.seed)
+        lens = [int(x) for x in np.clip(np.exp(rng.normal(np.log(16384), 1.0, B)), 2048, 131072)]
+        args.no_cpu_baseline = True
+    else:
+        lens = [L] * B
+    inp = synth.make_indexer_inputs(lens, next_n=n, seed=args.seed, device=dev)
     num_blocks = int(inp.block_tables.max().item()) + 1
     kv = synth.make_mla_cache(num_blocks, seed=args.seed, device=dev)
-    q_mla = synth.make_mla_query(B, H, seed=args.seed, device=dev)
+    q_mla = synth.make_mla_query(B * n, H, seed=args.seed, device=dev)
     scale = 192 ** -0.5
     max_ctx = inp.block_tables.shape[1] * 64
-    step = DsaDecodeStep(B, 1, max_ctx, num_heads=H, index_topk=K, device=dev, fused=not args.unfused)
-    seq = inp.context_lens
+    step = DsaDecodeStep(B, n, max_ctx, num_heads=H, index_topk=K, device=dev, fused=not args.unfused)
+    seq = step.expand_lens(inp.context_lens)   # per query token [B*n]
     bt = inp.block_tables
+    pt = bt.repeat_interleave(n, dim=0).contiguous() if n > 1 else bt
     from nanoengine_amd import ops
     torch.cuda.synchronize()
 
     def run(ev=None):
         # ev: [start, after sample, after filter, after finish, after repair, after MLA]
         if step.fused:
-            ops.indexer_topk(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt, max_ctx, K,
+            ops.indexer_topk(inp.q_fp8.view(B, n, 64, 128), inp.cache, inp.weights, seq.view(B, n), bt, max_ctx, K,
                              step.physical, step.logical, workspace=step.fused_workspace,
                              phase_events=ev[0:5] if ev is not None else None)
         else:
             if ev is not None:
                 ev[0].record()
-            ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+            ops.indexer_logits(inp.q_fp8.view(B, n, 64, 128), inp.cache, inp.weights, seq.view(B, n), bt,
                                max_ctx, out=step.logits)
             if ev is not None:
                 ev[1].record()
                 ev[2].record()
-            ops.topk_transform(step.logits, seq, bt, step.physical, 64, K, step.logical,
+            ops.topk_transform(step.logits, seq, pt, step.physical, 64, K, step.logical,
                                workspace=step.topk_workspace)
             if ev is not None:
                 ev[3].record()
@@ -169,20 +181,20 @@ def main():
     if args.only:
         run()
         torch.cuda.synchronize()
-        logits = torch.empty(B, max_ctx, dtype=torch.float32, device=dev) if args.only in ("indexer", "topk") else None
+        logits = torch.empty(B * n, max_ctx, dtype=torch.float32, device=dev) if args.only in ("indexer", "topk") else None
         if logits is not None:
-            ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+            ops.indexer_logits(inp.q_fp8.view(B, n, 64, 128), inp.cache, inp.weights, seq.view(B, n), bt,
                                max_ctx, out=logits)
         for _ in range(args.steps):
             if args.only == "fused":
-                ops.indexer_topk(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+                ops.indexer_topk(inp.q_fp8.view(B, n, 64, 128), inp.cache, inp.weights, seq.view(B, n), bt,
                                  max_ctx, K, step.physical, step.logical,
                                  workspace=getattr(step, "fused_workspace", None))
             elif args.only == "indexer":
-                ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1), bt,
+                ops.indexer_logits(inp.q_fp8.view(B, n, 64, 128), inp.cache, inp.weights, seq.view(B, n), bt,
                                    max_ctx, out=logits)
             elif args.only == "topk":
-                ops.topk_transform(logits, seq, bt, step.physical, 64, K, step.logical)
+                ops.topk_transform(logits, seq, pt, step.physical, 64, K, step.logical)
             else:
                 ops.sparse_mla_decode(q_mla, kv, step.physical, scale, out=step.out, lse=step.lse,
                                       num_splits=step.num_splits, workspace=step.workspace)
@@ -213,12 +225,12 @@ def main():
 
     total_tokens = sum(lens)
     # the filter pass reads every key page of every sequence (+ q and head weights)
-    idx_bytes = total_tokens * 132 + B * 64 * 128 + B * 64 * 4
+    idx_bytes = total_tokens * 132 + B * n * 64 * 128 + B * n * 64 * 4
     if not step.fused:
-        idx_bytes += B * max_ctx * 4  # the logits written
-    idx_flops = 2.0 * 64 * 128 * total_tokens
+        idx_bytes += B * n * max_ctx * 4  # the logits written
+    idx_flops = 2.0 * 64 * 128 * int(seq.sum().item())
     valid = int((step.physical >= 0).sum().item())
-    mla_bytes = valid * 656 + B * H * 576 * 2 + B * H * 512 * 2 + B * H * 4 + B * K * 4
+    mla_bytes = valid * 656 + B * n * H * 576 * 2 + B * n * H * 512 * 2 + B * n * H * 4 + B * n * K * 4
     mla_flops = 2.0 * H * (576 + 512) * valid
 
     def gbs(b, us):
@@ -257,12 +269,15 @@ def main():
         cpu = cpu_baseline(inp, kv, q_mla, lens, min(args.cpu_sample, B), scale, K)
 
     print(json.dumps({
-        "metric": METRIC, "value": round(B / (ms_per_step * 1e-3), 1), "unit": "tokens/s",
+        "metric": METRIC, "value": round(B * n / (ms_per_step * 1e-3), 1), "unit": "tokens/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "us_per_step": round(ms_per_step * 1e3, 1), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp8+bf16", "data": "synthetic",
-        "config": {"workload": "BASELINE config 2: full DSA decode step, one layer", "batch": B,
-                   "next_n": 1, "context_len": L, "index_topk": K, "indexer_heads": 64,
+        "config": {"workload": ("BASELINE config 2: full DSA decode step, one layer" if n == 1 else
+                                "BASELINE config 3: MTP verify step (next_n=2, causal draft lengths), one layer"),
+                   "batch": B, "next_n": n, "context_len": L if n == 1 else
+                   {"lognormal_median": 16384, "clip": [2048, 131072], "mean": round(sum(lens) / B)},
+                   "index_topk": K, "indexer_heads": 64,
                    "indexer_head_dim": 128, "mla_heads": H, "mla_dims": "576/512", "page_size": 64,
                    "kv_cache": "fp8 656 B/token (block stride 65 rows)", "indexer_cache": "fp8 132 B/token",
                    "parallelism": "single GPU"},
