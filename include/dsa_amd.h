@@ -230,6 +230,48 @@ DSA_API int dsa_indexer_k_store(const void* k, int64_t k_row_stride, const void*
                                 int slot_is_64, int num_tokens, uint8_t* cache, int page_size,
                                 void* stream);
 
+/* Indexer query prologue: RoPE -> Hadamard-128 -> UE8M0 fp8 quant -> gate scaling.
+ *   q            [num_tokens, num_heads, 128] bf16, contiguous, 16-byte aligned
+ *   gate         [num_tokens, num_heads] bf16, token stride gate_token_stride elements
+ *   cos_sin_cache [cache_positions, 64] f32 = [cos 0..31 | sin 0..31] per position
+ *   positions    [num_tokens] (int32, or int64 when pos_is_64), clamped to the cache
+ *   q_fp8        [num_tokens, num_heads, 128] e4m3fn codes (out)
+ *   weights_out  [num_tokens, num_heads] f32 = gate * weight_scale * sf (out)
+ * Dims 0..63 are interleaved (re, im) pairs when rope_interleaved (reordered to
+ * the half layout first), else already in the half layout. RoPE output and the
+ * Hadamard output (times 128^-0.5) are rounded to bf16; then per row
+ * sf = 2^ceil(log2(max(amax, 1e-4) / 448)), code = e4m3fn(x / sf).
+ * Replaces indexer_q_rope_hadamard_quant(query, gate_weight, weight_scale,
+ * cos_sin_cache, positions) (dlengine/runtime/kernel/jit/sgl/deepseek_v4.py:290-322,
+ * kernel jit/sgl/csrc/deepseek_v4/indexer_q.cuh:57-225; called at
+ * dlengine/runtime/layers/backends/dsa/indexer/lightning.py:1316-1325). */
+DSA_API int dsa_indexer_q_prologue(const void* q, const void* gate, int64_t gate_token_stride,
+                                   float weight_scale, const float* cos_sin_cache,
+                                   int64_t cache_positions, const void* positions, int pos_is_64,
+                                   int num_tokens, int num_heads, int rope_interleaved,
+                                   uint8_t* q_fp8, float* weights_out, void* stream);
+
+/* Indexer key transform + cache store: LayerNorm -> RoPE -> Hadamard-128 -> UE8M0
+ * fp8 quant -> split-page store.
+ *   key          [num_tokens, 128] bf16 (row stride key_row_stride elements, 16-byte aligned rows)
+ *   ln_weight, ln_bias [128] f32; eps the LayerNorm epsilon
+ *   cos_sin_cache, positions as for dsa_indexer_q_prologue; dims 0..63 of the
+ *                LayerNorm output are interleaved (re, im) pairs
+ *   slots        [num_tokens] flat slots (int32, or int64 when slot_is_64), < 0 skipped
+ *   cache        [pages, page_size*132] bytes, layout as for dsa_indexer_k_store
+ * The LayerNorm output and the RoPE output are rounded to bf16; the Hadamard
+ * output (times 128^-0.5) stays f32 for the quantisation.
+ * Replaces indexer_k_transform_store_fp8(key, weight, bias, eps, positions,
+ * cos_sin_cache, cache, slot_mapping, page_size)
+ * (dlengine/runtime/kernel/triton/generic/indexer_transform.py:156-288, called at
+ *  dlengine/runtime/layers/backends/dsa/indexer/lightning.py:1339-1350). */
+DSA_API int dsa_indexer_k_transform_store(const void* key, int64_t key_row_stride,
+                                          const float* ln_weight, const float* ln_bias, float eps,
+                                          const float* cos_sin_cache, int64_t cache_positions,
+                                          const void* positions, int pos_is_64, const void* slots,
+                                          int slot_is_64, int num_tokens, uint8_t* cache,
+                                          int page_size, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

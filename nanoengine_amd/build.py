@@ -14,7 +14,8 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libdsa_amd.so"
-SOURCES = ["capi.hip", "topk.hip", "indexer.hip", "sparse_mla.hip", "cache_store.hip"]
+SOURCES = ["capi.hip", "topk.hip", "indexer.hip", "sparse_mla.hip", "cache_store.hip",
+           "indexer_prologue.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -39,6 +40,7 @@ PER_FILE_FLAGS = {
     "indexer.hip": VGPR_FORM,
     "cache_store.hip": VGPR_FORM,
     "sparse_mla.hip": [],
+    "indexer_prologue.hip": [],
 }
 
 

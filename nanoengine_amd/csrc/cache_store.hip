@@ -14,33 +14,9 @@
 
 namespace dsa {
 
-// 2^ceil(log2(v)) for finite v > 0, exactly: v = 2^e * 1.m, ceil is e when the
-// mantissa is zero and e + 1 otherwise.
-__device__ __forceinline__ float pow2_ceil(float v) {
-  const uint32_t u = __float_as_uint(v);
-  int e = (int)((u >> 23) & 0xff);
-  const uint32_t m = u & 0x7fffffu;
-  if (e == 0) {  // subnormal: v = m * 2^-149
-    const int msb = 31 - __clz(m);
-    const int k = msb - 149 + ((m & (m - 1)) ? 1 : 0);
-    return ldexpf(1.f, k);
-  }
-  const int k = e - 127 + (m ? 1 : 0);
-  return ldexpf(1.f, k);
-}
-
-// Four floats -> four e4m3fn bytes (round to nearest even).
-__device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
-  return (uint32_t)w;
-}
-
 __device__ __forceinline__ int64_t load_slot(const void* slots, int slot_is_64, int i) {
   return slot_is_64 ? reinterpret_cast<const int64_t*>(slots)[i] : (int64_t)reinterpret_cast<const int32_t*>(slots)[i];
 }
-
-__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
 __global__ void __launch_bounds__(256)
 mla_kv_store_kernel(const uint16_t* __restrict__ kv, int64_t row_stride, const void* __restrict__ slots,

@@ -56,6 +56,30 @@ __device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
   return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
 }
 
+// 2^ceil(log2(v)) for finite v > 0, exactly: v = 2^e * 1.m, ceil is e when the
+// mantissa is zero and e + 1 otherwise.
+__device__ __forceinline__ float pow2_ceil(float v) {
+  const uint32_t u = __float_as_uint(v);
+  int e = (int)((u >> 23) & 0xff);
+  const uint32_t m = u & 0x7fffffu;
+  if (e == 0) {  // subnormal: v = m * 2^-149
+    const int msb = 31 - __clz(m);
+    const int k = msb - 149 + ((m & (m - 1)) ? 1 : 0);
+    return ldexpf(1.f, k);
+  }
+  const int k = e - 127 + (m ? 1 : 0);
+  return ldexpf(1.f, k);
+}
+
+// Four floats -> four e4m3fn bytes (round to nearest even).
+__device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
 // Dequantise 16 fp8 bytes (v4i) times `scale` into 16 bf16 (two v4i: dims
 // 0-7 and 8-15), one v_cvt_scalef32_pk_bf16_fp8 per pair of values. Exact for
 // power-of-two scales (an e4m3 value times 2^k is a bf16 value).

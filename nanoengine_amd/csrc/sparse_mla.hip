@@ -163,13 +163,6 @@ __device__ __forceinline__ int e8m0_for(float v) {
 __device__ __forceinline__ float e8m0_value(int e) { return __uint_as_float((uint32_t)e << 23); }
 __device__ __forceinline__ float e8m0_inv(int e) { return __uint_as_float((uint32_t)(254 - e) << 23); }
 
-// Four floats -> four e4m3fn bytes (round to nearest even).
-__device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
-  return (uint32_t)w;
-}
-
 __device__ __forceinline__ v8i lds_read32(const uint8_t* p) {
   const v4i a = *reinterpret_cast<const v4i*>(p);
   const v4i b = *reinterpret_cast<const v4i*>(p + 16);

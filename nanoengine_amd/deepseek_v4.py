@@ -1,7 +1,8 @@
-"""NSA top-k + page-table translation entry points, on MI355X.
+"""Indexer query prologue and NSA top-k + page-table translation entry points, on MI355X.
 
 Same signatures and error behaviour as
-dlengine/runtime/kernel/jit/sgl/deepseek_v4.py:324-400 (``topk_transform``,
+dlengine/runtime/kernel/jit/sgl/deepseek_v4.py:290-400
+(``indexer_q_rope_hadamard_quant``, ``topk_transform``,
 ``topk_transform_ragged``, ``topk_transform_512``). The selection is exact at
 every context length (the reference's fused kernel is exact only up to 16K and
 its ragged variant may differ by a few entries) and emits positions in
@@ -14,6 +15,30 @@ from typing import Optional
 import torch
 
 from . import ops
+
+
+def indexer_q_rope_hadamard_quant(query: torch.Tensor, gate_weight: torch.Tensor, weight_scale: float,
+                                  cos_sin_cache: torch.Tensor, positions: torch.Tensor,
+                                  rope_interleaved: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fuse RoPE-first, Hadamard-128, UE8M0 quant, and gate scaling.
+
+    query [T, H, 128] bf16 with dims 0..63 as interleaved RoPE pairs (the
+    reference's only layout; ``rope_interleaved=False`` takes them already in
+    the half layout), gate_weight [T, H] bf16, cos_sin_cache [max_pos, (1,) 64]
+    f32, positions [T] int32/int64. Returns (q_fp8 [T, H, 128] e4m3fn,
+    weights [T, H, 1] f32 = gate * weight_scale * q_scale)."""
+    if query.shape[-1] != 128:
+        raise ValueError(f"Indexer query head dim must be 128, got {query.shape[-1]}")
+    if gate_weight.shape != query.shape[:-1]:
+        raise ValueError(
+            f"gate weight shape {tuple(gate_weight.shape)} does not match "
+            f"query shape {tuple(query.shape[:-1])}")
+    query = query.contiguous()
+    q_fp8 = torch.empty_like(query, dtype=torch.float8_e4m3fn)
+    weights_out = torch.empty((*query.shape[:-1], 1), dtype=torch.float32, device=query.device)
+    ops.indexer_q_prologue(query, gate_weight, weight_scale, cos_sin_cache, positions, q_fp8, weights_out,
+                           rope_interleaved)
+    return q_fp8, weights_out
 
 
 def topk_transform(scores: torch.Tensor, seq_lens: torch.Tensor, page_tables: torch.Tensor,

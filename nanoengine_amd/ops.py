@@ -370,3 +370,63 @@ def indexer_k_store(key: torch.Tensor, cache: torch.Tensor, slot_mapping: torch.
     dev = _check_cuda(key, cache, slots)
     _lib.call("dsa_indexer_k_store", key.data_ptr(), key.stride(0), slots.data_ptr(), is64, key.shape[0],
               cache.data_ptr(), int(page_size), _stream(dev))
+
+
+# --------------------------------------------------------------------------- indexer prologue
+def _rope_cache(cos_sin_cache: torch.Tensor) -> torch.Tensor:
+    cs = cos_sin_cache.reshape(cos_sin_cache.shape[0], -1)
+    _require(cs.shape[1] == 64 and cs.dtype == torch.float32,
+             f"cos_sin_cache must be float32 [max_pos, 64], got {tuple(cos_sin_cache.shape)} {cos_sin_cache.dtype}")
+    return cs.contiguous()
+
+
+def _positions(positions: torch.Tensor, n: int) -> tuple[torch.Tensor, int]:
+    _require(positions.dim() == 1 and positions.shape[0] == n, f"positions must be 1-D of length {n}")
+    _require(positions.dtype in (torch.int32, torch.int64), f"positions dtype {positions.dtype}")
+    p = positions.contiguous()
+    return p, int(p.dtype == torch.int64)
+
+
+def indexer_q_prologue(query: torch.Tensor, gate_weight: torch.Tensor, weight_scale: float,
+                       cos_sin_cache: torch.Tensor, positions: torch.Tensor, q_fp8: torch.Tensor,
+                       weights_out: torch.Tensor, rope_interleaved: bool = True) -> None:
+    """RoPE -> Hadamard-128 -> UE8M0 fp8 quant -> gate scaling of the indexer query
+    (see dsa_indexer_q_prologue). query [T, H, 128] bf16 contiguous; gate_weight
+    [T, H] bf16 (token stride free); q_fp8 [T, H, 128] float8_e4m3fn (or uint8);
+    weights_out [T, H] (or [T, H, 1]) float32, contiguous."""
+    _require(query.dim() == 3 and query.shape[-1] == INDEXER_HEAD_DIM and query.dtype == torch.bfloat16
+             and query.is_contiguous(), "query must be contiguous bf16 [T, H, 128]", ValueError)
+    t, h = query.shape[0], query.shape[1]
+    _require(gate_weight.shape == (t, h) and gate_weight.dtype == torch.bfloat16 and gate_weight.stride(1) == 1,
+             f"gate_weight must be bf16 [{t}, {h}] with a contiguous last dim", ValueError)
+    _require(q_fp8.shape == query.shape and q_fp8.dtype in (torch.float8_e4m3fn, torch.uint8)
+             and q_fp8.is_contiguous(), "q_fp8 must be contiguous fp8 [T, H, 128]", ValueError)
+    _require(weights_out.numel() == t * h and weights_out.dtype == torch.float32 and weights_out.is_contiguous(),
+             "weights_out must be contiguous float32 with T*H entries", ValueError)
+    cs = _rope_cache(cos_sin_cache)
+    pos, pos64 = _positions(positions, t)
+    dev = _check_cuda(query, gate_weight, q_fp8, weights_out, cs, pos)
+    _lib.call("dsa_indexer_q_prologue", query.data_ptr(), gate_weight.data_ptr(), gate_weight.stride(0),
+              float(weight_scale), cs.data_ptr(), cs.shape[0], pos.data_ptr(), pos64, t, h, int(bool(rope_interleaved)),
+              _as_bytes(q_fp8).data_ptr(), weights_out.data_ptr(), _stream(dev))
+
+
+def indexer_k_transform_store(key: torch.Tensor, ln_weight: torch.Tensor, ln_bias: torch.Tensor, eps: float,
+                              positions: torch.Tensor, cos_sin_cache: torch.Tensor, cache: torch.Tensor,
+                              slot_mapping: torch.Tensor, page_size: int) -> None:
+    """LayerNorm -> RoPE -> Hadamard-128 -> UE8M0 fp8 quant -> split-page store of
+    indexer keys [T, 128] bf16 (see dsa_indexer_k_transform_store)."""
+    _require(key.dim() == 2 and key.shape[1] == INDEXER_HEAD_DIM and key.dtype == torch.bfloat16
+             and key.stride(1) == 1, "fused Indexer K path requires a bfloat16 [T, 128] key", ValueError)
+    lw = ln_weight.to(torch.float32).contiguous()
+    lb = ln_bias.to(torch.float32).contiguous()
+    _require(lw.numel() == INDEXER_HEAD_DIM and lb.numel() == INDEXER_HEAD_DIM, "LayerNorm weight/bias must have 128 entries")
+    _require(cache.dtype == torch.uint8 and cache.is_contiguous()
+             and cache.numel() % (page_size * INDEXER_ROW_BYTES) == 0, "cache must be contiguous uint8 pages")
+    cs = _rope_cache(cos_sin_cache)
+    pos, pos64 = _positions(positions, key.shape[0])
+    slots, is64 = _slots(slot_mapping, key.shape[0])
+    dev = _check_cuda(key, lw, lb, cs, pos, slots, cache)
+    _lib.call("dsa_indexer_k_transform_store", key.data_ptr(), key.stride(0), lw.data_ptr(), lb.data_ptr(),
+              float(eps), cs.data_ptr(), cs.shape[0], pos.data_ptr(), pos64, slots.data_ptr(), is64, key.shape[0],
+              cache.data_ptr(), int(page_size), _stream(dev))

@@ -26,6 +26,8 @@ __all__ = [
     "expand_decode_context_lens", "indexer_logits", "indexer_logits_bruteforce",
     "topk_select", "topk_transform", "topk_transform_ragged",
     "topk_indices_to_physical", "sparse_mla_decode", "indexer_decode_topk",
+    "rope_cos_sin_cache", "interleaved_to_half", "rope_neox", "hadamard128", "f32_tree_sum128",
+    "indexer_q_prologue", "indexer_k_transform",
 ]
 
 FP8_MAX = 448.0
@@ -99,9 +101,13 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
 
 def ue8m0_ceil(scale: np.ndarray) -> np.ndarray:
     """Round a positive scale up to a power of two (UE8M0): lightning.py:91-92,
-    fp8_utils.py:27-29 ``2^ceil(log2(s))``."""
+    fp8_utils.py:27-29 ``2^ceil(log2(s))``, and the exponent-plus-carry form of
+    ``cast_to_ue8m0`` (jit/sgl/include/sgl_kernel/deepseek_v4/fp8_utils.cuh:20-26).
+    Exact: from the binary exponent, not a floating log2."""
     s = np.asarray(scale, dtype=np.float32)
-    return np.exp2(np.ceil(np.log2(s))).astype(np.float32)
+    m, e = np.frexp(s.astype(np.float64))          # s = m * 2^e, m in [0.5, 1)
+    k = np.where(m == 0.5, e - 1, e)               # exact power of two: 2^(e-1)
+    return np.ldexp(np.float64(1.0), k).astype(np.float32)
 
 
 # --------------------------------------------------------------------------- indexer formats
@@ -396,3 +402,118 @@ def sparse_mla_decode(q: np.ndarray, kv_rows: np.ndarray, indices: np.ndarray,
         o[t] = ((p / den) @ kv[:, :d_v]).astype(np.float32)
         lse[t] = (m[:, 0] + np.log(den[:, 0])).astype(np.float32)
     return o, lse
+
+
+# --------------------------------------------------------------------------- indexer prologue
+# The reference leaves the f32 summation order of its Hadamard and LayerNorm
+# unspecified (a butterfly in indexer_q.cuh:164-193, tl.sum in
+# indexer_transform.py:177-181, 223-232). The functions below fix one order and
+# compute in IEEE f32 without fused multiply-adds, so a kernel using the same
+# order matches them bit for bit; the tests pin them against float64 library
+# routines (scipy's Hadamard matrix, complex multiplication, LayerNorm).
+_INV_SQRT128 = np.float32(0.0883883461356163)     # f32 nearest to 128^-0.5
+
+
+def rope_cos_sin_cache(max_pos: int, rotary_dim: int = 64, base: float = 10000.0) -> np.ndarray:
+    """[max_pos, rotary_dim] f32 = [cos | sin] of t * inv_freq (rotary_embedding.py:33-40)."""
+    inv_freq = (1.0 / (np.float32(base) ** (np.arange(0, rotary_dim, 2, dtype=np.float32) / rotary_dim)))
+    freqs = np.arange(max_pos, dtype=np.float32)[:, None] * inv_freq.astype(np.float32)[None, :]
+    return np.concatenate([np.cos(freqs), np.sin(freqs)], axis=-1).astype(np.float32)
+
+
+def interleaved_to_half(x: np.ndarray) -> np.ndarray:
+    """[..., 2m] interleaved (re, im) pairs -> [re 0..m-1 | im 0..m-1] (lightning.py:110-113)."""
+    x = np.asarray(x)
+    return np.swapaxes(x.reshape(*x.shape[:-1], -1, 2), -1, -2).reshape(x.shape)
+
+
+def rope_neox(x_half: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """NeoX rotation in f32 (rotary_embedding.py:10-18): x = [x1 | x2],
+    y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin. cos/sin broadcast over x1."""
+    x = np.asarray(x_half, dtype=np.float32)
+    h = x.shape[-1] // 2
+    x1, x2 = x[..., :h], x[..., h:]
+    cos = np.asarray(cos, dtype=np.float32)
+    sin = np.asarray(sin, dtype=np.float32)
+    y1 = x1 * cos - x2 * sin
+    y2 = x2 * cos + x1 * sin
+    return np.concatenate([y1, y2], axis=-1).astype(np.float32)
+
+
+def hadamard128(x: np.ndarray) -> np.ndarray:
+    """128-point Walsh-Hadamard transform times 128^-0.5 in f32: stages h = 1, 2,
+    ..., 64, each (a, b) -> (a + b, a - b) (indexer_q.cuh:164-198)."""
+    y = np.array(x, dtype=np.float32, copy=True)
+    n = y.shape[-1]
+    assert n == 128
+    h = 1
+    while h < n:
+        v = y.reshape(*y.shape[:-1], n // (2 * h), 2, h)
+        a = v[..., 0, :].copy()
+        b = v[..., 1, :].copy()
+        v[..., 0, :] = a + b
+        v[..., 1, :] = a - b
+        h *= 2
+    return (y * _INV_SQRT128).astype(np.float32)
+
+
+def f32_tree_sum128(x: np.ndarray) -> np.ndarray:
+    """Sum over the last axis (128) in f32: element e = 8j + i, in-j tree over i
+    ((i, i+4), (i, i+2), (i, i+1)), then a butterfly over j (xor 1, 2, 4, 8)."""
+    v = np.asarray(x, dtype=np.float32).reshape(*np.shape(x)[:-1], 16, 8)
+    v = v[..., :4] + v[..., 4:]
+    v = v[..., :2] + v[..., 2:]
+    s = (v[..., 0] + v[..., 1]).astype(np.float32)           # [..., 16]
+    j = np.arange(16)
+    for m in (1, 2, 4, 8):
+        s = (s + s[..., j ^ m]).astype(np.float32)
+    return s[..., 0]
+
+
+def _quant_ue8m0_f32(x: np.ndarray):
+    amax = np.maximum(np.abs(x).max(axis=-1), np.float32(1e-4)).astype(np.float32)
+    sf = ue8m0_ceil((amax / np.float32(FP8_MAX)).astype(np.float32))
+    codes = fp8_e4m3fn_encode(x * (np.float32(1.0) / sf)[..., None])
+    return codes, sf
+
+
+def indexer_q_prologue(q_bf16: np.ndarray, gate_bf16: np.ndarray, weight_scale: float, cos_sin: np.ndarray,
+                       positions: np.ndarray, rope_interleaved: bool = True):
+    """Indexer query prologue (indexer_q.cuh:57-225 as instantiated at
+    jit/sgl/deepseek_v4.py:153-165, 290-322; unfused steps lightning.py:720-755,
+    1327-1337 and their composition in tests/test_indexer_transform.py:72-116).
+
+    q_bf16 [T, H, 128] uint16, gate_bf16 [T, H] uint16, cos_sin [P, 64] f32,
+    positions [T]. Returns (codes uint8 [T, H, 128], weights f32 [T, H])."""
+    x = bf16_to_f32(q_bf16).astype(np.float32)
+    rope = x[..., :64]
+    if rope_interleaved:
+        rope = interleaved_to_half(rope)
+    cs = np.asarray(cos_sin, dtype=np.float32)[np.asarray(positions, dtype=np.int64)]   # [T, 64]
+    rot = rope_neox(rope, cs[:, None, :32], cs[:, None, 32:])
+    x = np.concatenate([bf16_to_f32(f32_to_bf16(rot)), x[..., 64:]], axis=-1)
+    y = bf16_to_f32(f32_to_bf16(hadamard128(x)))
+    codes, sf = _quant_ue8m0_f32(y)
+    g = bf16_to_f32(gate_bf16).astype(np.float32)
+    weights = (g * np.float32(weight_scale)).astype(np.float32) * sf
+    return codes, weights.astype(np.float32)
+
+
+def indexer_k_transform(key_bf16: np.ndarray, ln_w: np.ndarray, ln_b: np.ndarray, eps: float,
+                        cos_sin: np.ndarray, positions: np.ndarray):
+    """Indexer key transform (indexer_transform.py:156-260): LayerNorm (biased
+    variance, 1/sqrt(var + eps)) rounded to bf16, RoPE on the interleaved
+    leading 64 dims rounded to bf16, Hadamard kept in f32, UE8M0 quantisation.
+
+    key_bf16 [T, 128] uint16. Returns (codes uint8 [T, 128], scales f32 [T])."""
+    x = bf16_to_f32(key_bf16).astype(np.float32)
+    mean = (f32_tree_sum128(x) * np.float32(1.0 / 128.0)).astype(np.float32)
+    c = (x - mean[:, None]).astype(np.float32)
+    var = (f32_tree_sum128(c * c) * np.float32(1.0 / 128.0)).astype(np.float32)
+    inv_std = (np.float32(1.0) / np.sqrt((var + np.float32(eps)).astype(np.float32))).astype(np.float32)
+    y = ((c * inv_std[:, None]).astype(np.float32) * np.asarray(ln_w, dtype=np.float32)).astype(np.float32)
+    y = bf16_to_f32(f32_to_bf16(y + np.asarray(ln_b, dtype=np.float32)))
+    cs = np.asarray(cos_sin, dtype=np.float32)[np.asarray(positions, dtype=np.int64)]
+    rot = rope_neox(interleaved_to_half(y[:, :64]), cs[:, :32], cs[:, 32:])
+    y = np.concatenate([bf16_to_f32(f32_to_bf16(rot)), y[:, 64:]], axis=-1)
+    return _quant_ue8m0_f32(hadamard128(y))
