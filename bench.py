@@ -114,6 +114,46 @@ def cpu_baseline(inp, kv, q_mla, lens, sample, scale, topk):
                       f"logits + exact top-{topk} + transform + sparse MLA), {dt:.1f} s"}
 
 
+def prologue_stages(T, dev, seed, reps=50):
+    """Average launch time of the indexer prologue kernels for the step's T query
+    tokens (they run before the step, so they are reported beside it, not in it):
+    the query transform over T x 64 heads and the key transform + store of T keys."""
+    import torch
+
+    from nanoengine_amd import ops
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    q = torch.randn(T, 64, 128, generator=g).to(torch.bfloat16).to(dev)
+    gate = torch.randn(T, 64, generator=g).to(torch.bfloat16).to(dev)
+    key = torch.randn(T, 128, generator=g).to(torch.bfloat16).to(dev)
+    cs = torch.randn(131072, 64, generator=g).to(dev)
+    pos = torch.randint(0, 131072, (T,), generator=g).to(dev)
+    slots = torch.randperm(T * 4, generator=g)[:T].to(torch.int32).to(dev)
+    lw, lb = torch.ones(128, device=dev), torch.zeros(128, device=dev)
+    q8 = torch.empty(T, 64, 128, dtype=torch.uint8, device=dev)
+    w = torch.empty(T, 64, dtype=torch.float32, device=dev)
+    cache = torch.zeros((T * 4 + 63) // 64 * 64 * 132, dtype=torch.uint8, device=dev)
+    calls = {
+        "indexer_q_prologue": (lambda: ops.indexer_q_prologue(q, gate, 0.01, cs, pos, q8, w),
+                               T * 64 * (256 + 128 + 4 + 2) + T * 256),
+        "indexer_k_transform_store": (lambda: ops.indexer_k_transform_store(key, lw, lb, 1e-6, pos, cs, cache,
+                                                                            slots, 64), T * (256 + 132 + 256)),
+    }
+    out = {}
+    for name, (fn, nbytes) in calls.items():
+        for _ in range(5):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        out[name] = {"us": round(us, 2), "tokens": T, "bytes": nbytes,
+                     "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -263,6 +303,8 @@ def main():
                 "frac": r4(achieved / HBM_PEAK_GBS), "traffic": pmc_traffic() if step.fused else None,
                 "kernel": "indexer_logits_kernel<1, kIdxFilter>" if step.fused else "indexer_logits_kernel<1, kIdxStore>",
                 "bytes_per_launch": idx_bytes, "avg_launch_us": round(filt_us, 2)}
+
+    stages["outside_step"] = prologue_stages(B * n, dev, args.seed)
 
     cpu = None
     if not args.no_cpu_baseline:

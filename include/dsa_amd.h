@@ -272,6 +272,24 @@ DSA_API int dsa_indexer_k_transform_store(const void* key, int64_t key_row_strid
                                           int slot_is_64, int num_tokens, uint8_t* cache,
                                           int page_size, void* stream);
 
+/* Ragged fp8 MQA logits (prefill indexer).
+ *   q        [num_rows, 64, 128] e4m3fn, contiguous, 16-byte aligned
+ *   kv       [num_keys, 128] e4m3fn, contiguous, 16-byte aligned; kv_scale [num_keys] f32
+ *   weights  [num_rows, 64] f32 (row stride weights_stride)
+ *   ks, ke   [num_rows] int32: row i scores keys [ks[i], ke[i]) (0 <= ks, ke <= num_keys)
+ *   logits   [num_rows, logits_stride] f32 (out), columns [0, num_cols), num_cols >= num_keys
+ * logits[i, j] = sum_h w[i,h] * relu(q[i,h,:] . kv[j,:]) * kv_scale[j] inside the
+ * window; with clean_logits every other column < num_cols is -inf, otherwise it
+ * is not written. num_heads must be 64.
+ * Replaces deep_gemm.fp8_mqa_logits(q, (kv, kv_scale), weights, ks, ke, clean_logits)
+ * (third-party DeepGEMM, called at dlengine/runtime/layers/backends/dsa/indexer/
+ *  lightning.py:1212-1219). */
+DSA_API int dsa_mqa_logits(const uint8_t* q, const uint8_t* kv, const float* kv_scale,
+                           const float* weights, int64_t weights_stride, const int32_t* ks,
+                           const int32_t* ke, int num_rows, int64_t num_keys, int num_heads,
+                           float* logits, int64_t logits_stride, int64_t num_cols,
+                           int clean_logits, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

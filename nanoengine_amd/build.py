@@ -15,7 +15,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libdsa_amd.so"
 SOURCES = ["capi.hip", "topk.hip", "indexer.hip", "sparse_mla.hip", "cache_store.hip",
-           "indexer_prologue.hip"]
+           "indexer_prologue.hip", "prefill_logits.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -41,6 +41,7 @@ PER_FILE_FLAGS = {
     "cache_store.hip": VGPR_FORM,
     "sparse_mla.hip": [],
     "indexer_prologue.hip": [],
+    "prefill_logits.hip": VGPR_FORM,
 }
 
 

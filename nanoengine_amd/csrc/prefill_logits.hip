@@ -1,0 +1,248 @@
+// Ragged fp8 MQA logits for the prefill indexer, for gfx950:
+//
+//   logits[i, j] = sum_h w[i, h] * relu(q[i, h, :] . kv[j, :]) * kv_scale[j],  ks[i] <= j < ke[i]
+//
+// (the contraction of deep_gemm.fp8_mqa_logits as called at
+// dlengine/runtime/layers/backends/dsa/indexer/lightning.py:1212-1219; the
+// score definition is lightning.py:116-162).
+//
+// This is a GEMM of the (token, head) rows of q [M*64, 128] against the keys
+// [N, 128] with a ReLU-weighted head reduction in the epilogue, so it runs on
+// v_mfma_scale_f32_16x16x128_f8f6f4 (unit scales; K = 128 is one instruction).
+// A workgroup (8 waves) owns 16 query tokens and one chunk of keys; each wave
+// keeps the A operand of its 2 tokens (2 x 64 heads x 128 B) resident in
+// registers for the whole chunk. Keys stream through LDS in 64-key stages
+// (8 KB, three buffers): every wave issues one 1 KB global->LDS copy per
+// stage, already in the lane order of the MFMA B operand, so the operand is
+// two conflict-free ds_read_b128 per 16 keys. Per 16 keys and token: 4 MFMAs
+// (64 heads), ReLU + weight on the 16 accumulators a lane holds, then a
+// 2-shuffle butterfly over the 4 key groups of a stage leaves lane l with key
+// l of the stage: one coalesced 256-byte store per token and stage.
+//
+// Grid: token blocks x key chunks, with the chunk count a multiple of 8 and
+// chunk c placed on XCD c % 8 (workgroups are dealt to the 8 XCDs round
+// robin), so the workgroups sharing a chunk's keys share one L2.
+#include <algorithm>
+
+#include "dsa_common.h"
+#include "../../include/dsa_amd.h"
+
+namespace dsa {
+namespace {
+
+constexpr int kPfThreads = 512;
+constexpr int kPfWaves = kPfThreads / 64;
+constexpr int kPfTokensPerWave = 2;
+constexpr int kPfTokens = kPfWaves * kPfTokensPerWave;  // 16 per workgroup
+constexpr int kPfStageKeys = 64;
+constexpr int kPfStageBytes = kPfStageKeys * 128;       // 8 KB of keys
+constexpr int kPfBufs = 3;
+constexpr int kPfHeads = 64;
+
+struct PfLds {
+  uint8_t key[kPfBufs][kPfStageBytes];
+  float scale[kPfBufs][kPfStageKeys];
+};
+
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)reinterpret_cast<uintptr_t>(p); }
+
+__device__ __forceinline__ v8i load32B(const uint8_t* p) {
+  const v4i a = *reinterpret_cast<const v4i*>(p);
+  const v4i b = *reinterpret_cast<const v4i*>(p + 16);
+  v8i r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+__device__ __forceinline__ float relu(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, 3.402823466e38f); }
+
+// Issue this wave's share of stage `kb` (keys kb .. kb+63) into LDS buffer `buf`:
+// wave w copies 16 B per lane of key group w/2, half w%2 (lane l: key
+// kb + 16(w/2) + l%16, bytes 32(l/16) + 16(w%2) .. +16) to key[buf] +
+// 2048(w/2) + 1024(w%2) + 16 l; lanes 8w .. 8w+7 copy the scales of keys
+// kb + 8w .. +8. Keys past n_keys read key n_keys - 1 (their logits are never stored).
+__device__ __forceinline__ void issue_stage(PfLds* lds, int buf, int64_t kb, int64_t n_keys, const uint8_t* kv,
+                                            const float* kv_scale, int wave, int lane) {
+  const int g = wave >> 1, hf = wave & 1;
+  int64_t key = kb + g * 16 + (lane & 15);
+  key = key < n_keys ? key : n_keys - 1;
+  dma16(kv + key * 128 + (lane >> 4) * 32 + hf * 16, lds_addr(&lds->key[buf][g * 2048 + hf * 1024]));
+  int64_t sk = kb + lane;
+  sk = sk < n_keys ? sk : n_keys - 1;
+  if ((lane >> 3) == wave) dma4(kv_scale + sk, lds_addr(&lds->scale[buf][0]));
+}
+
+template <bool kPaged>
+__global__ void __launch_bounds__(kPfThreads, 1)
+mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv, const float* __restrict__ kv_scale,
+                  const float* __restrict__ weights, int64_t w_stride, const int32_t* __restrict__ ks,
+                  const int32_t* __restrict__ ke, int M, int64_t n_keys, int token_blocks, int64_t chunk_keys,
+                  float* __restrict__ logits, int64_t logits_stride) {
+  __shared__ PfLds lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // workgroup -> (token block, chunk): XCD b % 8 takes chunks c with c % 8 == b % 8
+  const int b = blockIdx.x;
+  const int r = b >> 3;
+  const int tb = r % token_blocks;
+  const int chunk = (r / token_blocks) * 8 + (b & 7);
+  const int r0 = tb * kPfTokens;
+  // key range of the block's 16 rows, intersected with the chunk
+  int lo_i = INT32_MAX, hi_i = INT32_MIN;
+  if (lane < kPfTokens && r0 + lane < M) {
+    lo_i = ks[r0 + lane];
+    hi_i = ke[r0 + lane];
+  }
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    lo_i = min(lo_i, __shfl_xor(lo_i, m, 64));
+    hi_i = max(hi_i, __shfl_xor(hi_i, m, 64));
+  }
+  lo_i = __builtin_amdgcn_readfirstlane(lo_i);
+  hi_i = __builtin_amdgcn_readfirstlane(hi_i);
+  const int64_t c0 = (int64_t)chunk * chunk_keys;
+  int64_t lo = max((int64_t)lo_i, c0), hi = min(min((int64_t)hi_i, c0 + chunk_keys), n_keys);
+  if (lo >= hi) return;
+  lo &= ~(int64_t)(kPfStageKeys - 1);
+  const int nstages = (int)((hi - lo + kPfStageKeys - 1) / kPfStageKeys);
+
+  // this wave's two tokens: A operands (head ht*16 + lane%16, bytes 32(lane/16) .. +32) and weights
+  int row[kPfTokensPerWave], rks[kPfTokensPerWave], rke[kPfTokensPerWave];
+  v8i qa[kPfTokensPerWave][4];
+  float w[kPfTokensPerWave][4][4];
+#pragma unroll
+  for (int j = 0; j < kPfTokensPerWave; ++j) {
+    const int rr = r0 + wave * kPfTokensPerWave + j;
+    row[j] = rr;
+    const bool ok = rr < M;
+    const int rc = ok ? rr : M - 1;
+    rks[j] = ok ? ks[rc] : 0;
+    rke[j] = ok ? ke[rc] : 0;
+    const uint8_t* qb = q + (int64_t)rc * kPfHeads * 128;
+    const float* wb = weights + (int64_t)rc * w_stride;
+#pragma unroll
+    for (int ht = 0; ht < 4; ++ht) {
+      qa[j][ht] = load32B(qb + (ht * 16 + (lane & 15)) * 128 + (lane >> 4) * 32);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[j][ht][e] = wb[ht * 16 + (lane >> 4) * 4 + e];
+    }
+  }
+  issue_stage(&lds, 0, lo, n_keys, kv, kv_scale, wave, lane);
+  if (nstages > 1) issue_stage(&lds, 1, lo + kPfStageKeys, n_keys, kv, kv_scale, wave, lane);
+  // the query loads above are ordinary loads: make the compiler's count start from zero
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+
+  for (int s = 0; s < nstages; ++s) {
+    // stage s landed for every wave; every wave is done reading buffer (s + 2) % 3
+    if (s + 1 < nstages) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int buf = s % kPfBufs;
+    const int64_t kb = lo + (int64_t)s * kPfStageKeys;
+    const uint8_t* kbuf = lds.key[buf];
+    float part[kPfTokensPerWave][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const v4i b0 = *reinterpret_cast<const v4i*>(kbuf + g * 2048 + 16 * lane);
+      const v4i b1 = *reinterpret_cast<const v4i*>(kbuf + g * 2048 + 1024 + 16 * lane);
+      v8i kb8;
+      kb8[0] = b0[0]; kb8[1] = b0[1]; kb8[2] = b0[2]; kb8[3] = b0[3];
+      kb8[4] = b1[0]; kb8[5] = b1[1]; kb8[6] = b1[2]; kb8[7] = b1[3];
+#pragma unroll
+      for (int j = 0; j < kPfTokensPerWave; ++j) {
+        v4f c[4];
+#pragma unroll
+        for (int ht = 0; ht < 4; ++ht)
+          c[ht] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j][ht], kb8, (v4f){0.f, 0.f, 0.f, 0.f},
+                                                                  0, 0, 0, 127, 0, 127);
+        // c[ht][e]: head ht*16 + (lane/16)*4 + e, key kb + 16g + lane%16
+        float acc = 0.f;
+#pragma unroll
+        for (int ht = 0; ht < 4; ++ht)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = fmaf(w[j][ht][e], relu(c[ht][e]), acc);
+        part[j][g] = acc;
+      }
+    }
+    const float sc = lds.scale[buf][lane];
+    const int64_t key = kb + lane;
+#pragma unroll
+    for (int j = 0; j < kPfTokensPerWave; ++j) {
+      // butterfly over the four 16-lane groups: lane group q keeps key group q
+      const bool hi32 = lane & 32;
+      const float s0 = hi32 ? part[j][0] : part[j][2];
+      const float s1 = hi32 ? part[j][1] : part[j][3];
+      const float k0 = (hi32 ? part[j][2] : part[j][0]) + __shfl_xor(s0, 32, 64);
+      const float k1 = (hi32 ? part[j][3] : part[j][1]) + __shfl_xor(s1, 32, 64);
+      const bool hi16 = lane & 16;
+      const float v = (hi16 ? k1 : k0) + __shfl_xor(hi16 ? k0 : k1, 16, 64);
+      if (key >= rks[j] && key < rke[j] && key < hi)
+        __builtin_nontemporal_store(v * sc, logits + (int64_t)row[j] * logits_stride + key);
+    }
+    if (s + 2 < nstages) issue_stage(&lds, (s + 2) % kPfBufs, kb + 2 * kPfStageKeys, n_keys, kv, kv_scale, wave, lane);
+  }
+}
+
+// logits[i, j] = -inf for j outside [ks[i], ke[i]), j < n_cols.
+__global__ void __launch_bounds__(256)
+mqa_logits_clean_kernel(const int32_t* __restrict__ ks, const int32_t* __restrict__ ke, int rows, int64_t n_cols,
+                        float* __restrict__ logits, int64_t logits_stride) {
+  for (int i = blockIdx.y; i < rows; i += gridDim.y) {
+    const int64_t a = ks[i], e = ke[i];
+    float* rowp = logits + (int64_t)i * logits_stride;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n_cols; j += (int64_t)gridDim.x * blockDim.x)
+      if (j < a || j >= e) rowp[j] = -__builtin_inff();
+  }
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" {
+
+int dsa_mqa_logits(const uint8_t* q, const uint8_t* kv, const float* kv_scale, const float* weights,
+                   int64_t weights_stride, const int32_t* ks, const int32_t* ke, int num_rows, int64_t num_keys,
+                   int num_heads, float* logits, int64_t logits_stride, int64_t num_cols, int clean_logits,
+                   void* stream) {
+  using namespace dsa;
+  if (num_rows < 0 || num_keys < 0 || num_cols < num_keys || logits_stride < num_cols || weights_stride < num_heads)
+    return set_error(kInvalidArgument, "dsa_mqa_logits: bad sizes");
+  if (num_heads != kPfHeads) return set_error(kUnsupported, "dsa_mqa_logits: num_heads must be 64, got %d", num_heads);
+  if (num_rows == 0) return kOk;
+  if (!q || !weights || !ks || !ke || !logits || (num_keys > 0 && (!kv || !kv_scale)))
+    return set_error(kInvalidArgument, "dsa_mqa_logits: null pointer");
+  if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(kv) & 15) ||
+      (reinterpret_cast<uintptr_t>(kv_scale) & 3) || (reinterpret_cast<uintptr_t>(weights) & 3))
+    return set_error(kInvalidArgument, "dsa_mqa_logits: q and kv must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (clean_logits && num_cols > 0) {
+    const int gx = (int)std::min<int64_t>((num_cols + 255) / 256, 64);
+    hipLaunchKernelGGL(mqa_logits_clean_kernel, dim3(gx, std::min(num_rows, 65535)), dim3(256), 0, st, ks, ke,
+                       num_rows, num_cols, logits, logits_stride);
+    if (int rc = check_launch("dsa_mqa_logits (clean)")) return rc;
+  }
+  if (num_keys == 0) return kOk;
+  const int token_blocks = (num_rows + kPfTokens - 1) / kPfTokens;
+  // chunks: a multiple of 8 (one XCD each), enough workgroups for the 256 CUs
+  int64_t chunks = 8;
+  while ((int64_t)token_blocks * chunks < 1024 && chunks * 64 * 8 <= num_keys) chunks *= 2;
+  int64_t chunk_keys = (num_keys + chunks - 1) / chunks;
+  chunk_keys = (chunk_keys + kPfStageKeys - 1) / kPfStageKeys * kPfStageKeys;
+  const int64_t grid = (int64_t)token_blocks * chunks;
+  if (grid > INT32_MAX) return set_error(kInvalidArgument, "dsa_mqa_logits: grid too large");
+  hipLaunchKernelGGL(mqa_logits_kernel<false>, dim3((unsigned)grid), dim3(kPfThreads), 0, st, q, kv, kv_scale,
+                     weights, weights_stride, ks, ke, num_rows, num_keys, token_blocks, chunk_keys, logits,
+                     logits_stride);
+  return check_launch("dsa_mqa_logits");
+}
+
+}  // extern "C"

@@ -1,9 +1,10 @@
-"""The three DeepGEMM entry points the DSA indexer calls, on MI355X.
+"""The four DeepGEMM entry points the DSA indexer calls, on MI355X.
 
 Same names, arguments and results as the calls at
 dlengine/runtime/layers/backends/dsa/indexer/lightning.py:633 (``get_num_sms``),
-:668-676 (``get_paged_mqa_logits_metadata``) and :1395-1406
-(``fp8_paged_mqa_logits``), so the caller's code stays unchanged.
+:668-676 (``get_paged_mqa_logits_metadata``), :1395-1406
+(``fp8_paged_mqa_logits``) and :1212-1219 (``fp8_mqa_logits``, prefill), so the
+caller's code stays unchanged.
 """
 from __future__ import annotations
 
@@ -57,4 +58,20 @@ def fp8_paged_mqa_logits(q_fp8: torch.Tensor, kv_cache: torch.Tensor, weights: t
     for j in range(n):
         ops.indexer_logits(q_fp8[:, j:j + 1].contiguous(), kv, w[:, j].contiguous(),
                            cl[:, j:j + 1].contiguous(), block_tables, max_context_len, out=rows[:, j])
+    return out
+
+
+def fp8_mqa_logits(q: torch.Tensor, kv: tuple[torch.Tensor, torch.Tensor], weights: torch.Tensor,
+                   cu_seq_len_k_start: torch.Tensor, cu_seq_len_k_end: torch.Tensor,
+                   clean_logits: bool = True) -> torch.Tensor:
+    """Ragged weighted-ReLU MQA logits for prefill.
+
+    q [M, 64, 128] float8_e4m3fn; kv = (keys [N, 128] float8_e4m3fn, scales [N] f32);
+    weights [M, 64] f32; cu_seq_len_k_start / _end [M] int32: row i scores keys
+    [start[i], end[i]). Returns logits [M, N] f32; with ``clean_logits`` every
+    entry outside a row's window is -inf, otherwise those entries are unspecified.
+    """
+    keys, scales = kv
+    out = torch.empty(q.shape[0], keys.shape[0], dtype=torch.float32, device=q.device)
+    ops.mqa_logits(q, keys, scales, weights, cu_seq_len_k_start, cu_seq_len_k_end, out, clean_logits)
     return out

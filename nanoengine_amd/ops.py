@@ -430,3 +430,29 @@ def indexer_k_transform_store(key: torch.Tensor, ln_weight: torch.Tensor, ln_bia
     _lib.call("dsa_indexer_k_transform_store", key.data_ptr(), key.stride(0), lw.data_ptr(), lb.data_ptr(),
               float(eps), cs.data_ptr(), cs.shape[0], pos.data_ptr(), pos64, slots.data_ptr(), is64, key.shape[0],
               cache.data_ptr(), int(page_size), _stream(dev))
+
+
+# --------------------------------------------------------------------------- prefill indexer
+def mqa_logits(q_fp8: torch.Tensor, kv_fp8: torch.Tensor, kv_scale: torch.Tensor, weights: torch.Tensor,
+               ks: torch.Tensor, ke: torch.Tensor, out: torch.Tensor, clean_logits: bool = True) -> None:
+    """Ragged fp8 MQA logits into out [M, >=N] f32 (see dsa_mqa_logits)."""
+    _require(q_fp8.dim() == 3 and q_fp8.shape[1] == INDEXER_HEADS and q_fp8.shape[2] == INDEXER_HEAD_DIM
+             and q_fp8.is_contiguous(), "q must be contiguous fp8 [M, 64, 128]", ValueError)
+    m = q_fp8.shape[0]
+    kv2 = kv_fp8.reshape(-1, INDEXER_HEAD_DIM)
+    _require(kv2.is_contiguous(), "kv must be contiguous fp8 [N, 128]", ValueError)
+    n = kv2.shape[0]
+    sc = kv_scale.reshape(-1)
+    _require(sc.numel() == n and sc.dtype == torch.float32 and sc.is_contiguous(),
+             "kv scales must be contiguous f32 [N]", ValueError)
+    _require(weights.shape == (m, INDEXER_HEADS) and weights.dtype == torch.float32 and weights.stride(1) == 1,
+             "weights must be f32 [M, 64]", ValueError)
+    for t in (ks, ke):
+        _require(t.dim() == 1 and t.shape[0] == m and t.dtype == torch.int32 and t.is_contiguous(),
+                 "k start/end must be contiguous int32 [M]", ValueError)
+    _require(out.dim() == 2 and out.shape[0] == m and out.shape[1] >= n and out.dtype == torch.float32
+             and out.stride(1) == 1, "out must be f32 [M, >=N]", ValueError)
+    dev = _check_cuda(q_fp8, kv2, sc, weights, ks, ke, out)
+    _lib.call("dsa_mqa_logits", _as_bytes(q_fp8).data_ptr(), _as_bytes(kv2).data_ptr(), sc.data_ptr(),
+              weights.data_ptr(), weights.stride(0), ks.data_ptr(), ke.data_ptr(), m, n, INDEXER_HEADS,
+              out.data_ptr(), out.stride(0), out.shape[1], int(bool(clean_logits)), _stream(dev))

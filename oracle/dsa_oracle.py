@@ -27,7 +27,8 @@ __all__ = [
     "topk_select", "topk_transform", "topk_transform_ragged",
     "topk_indices_to_physical", "sparse_mla_decode", "indexer_decode_topk",
     "rope_cos_sin_cache", "interleaved_to_half", "rope_neox", "hadamard128", "f32_tree_sum128",
-    "indexer_q_prologue", "indexer_k_transform",
+    "indexer_q_prologue", "indexer_k_transform", "mqa_logits", "gather_indexer_cache",
+    "prefill_ks_ke",
 ]
 
 FP8_MAX = 448.0
@@ -517,3 +518,66 @@ def indexer_k_transform(key_bf16: np.ndarray, ln_w: np.ndarray, ln_b: np.ndarray
     rot = rope_neox(interleaved_to_half(y[:, :64]), cs[:, :32], cs[:, 32:])
     y = np.concatenate([bf16_to_f32(f32_to_bf16(rot)), y[:, 64:]], axis=-1)
     return _quant_ue8m0_f32(hadamard128(y))
+
+
+# --------------------------------------------------------------------------- prefill indexer
+def gather_indexer_cache(cache: np.ndarray, block_table: np.ndarray, cu_seqlens_k: np.ndarray,
+                         page_size: int = 64, head_dim: int = 128):
+    """Paged split-layout cache -> contiguous ragged (keys uint8 [total_k, 128],
+    scales f32 [total_k]) (kernel/triton/generic/indexer_cache_gather.py:8-114):
+    ragged token cu[b] + t is token t of sequence b, read through block_table[b]."""
+    cu = np.asarray(cu_seqlens_k, dtype=np.int64)
+    total = int(cu[-1])
+    keys = np.zeros((total, head_dim), dtype=np.uint8)
+    scales = np.zeros(total, dtype=np.float32)
+    for b in range(len(cu) - 1):
+        for t in range(int(cu[b + 1] - cu[b])):
+            page = int(block_table[b, t // page_size])
+            off = t % page_size
+            keys[cu[b] + t] = cache[page, off * head_dim:(off + 1) * head_dim]
+            base = page_size * head_dim + off * 4
+            scales[cu[b] + t] = cache[page, base:base + 4].copy().view(np.float32)[0]
+    return keys, scales
+
+
+def prefill_ks_ke(cu_seqlens_q: np.ndarray, cu_seqlens_k: np.ndarray):
+    """Per-query ragged key window [ks, ke) of a chunked prefill
+    (lightning.py:1187-1209): query t of sequence b sees its cached prefix and
+    the fresh keys up to itself, ks = cu_k[b], ke = ks + (k_len - q_len) + local + 1."""
+    cq = np.asarray(cu_seqlens_q, dtype=np.int64)
+    ck = np.asarray(cu_seqlens_k, dtype=np.int64)
+    ks, ke = [], []
+    for b in range(len(cq) - 1):
+        qn, kn = cq[b + 1] - cq[b], ck[b + 1] - ck[b]
+        for t in range(qn):
+            ks.append(ck[b])
+            ke.append(ck[b] + (kn - qn) + t + 1)
+    return np.asarray(ks, dtype=np.int32), np.asarray(ke, dtype=np.int32)
+
+
+def mqa_logits(q_fp8: np.ndarray, kv_fp8: np.ndarray, kv_scale: np.ndarray, weights: np.ndarray,
+               ks: np.ndarray, ke: np.ndarray, clean_logits: bool = True) -> np.ndarray:
+    """Ragged fp8 MQA logits, the contract of ``deep_gemm.fp8_mqa_logits`` as
+    called at lightning.py:1212-1219 (third-party DeepGEMM, not vendored; the
+    score is lightning.py:116-131 ``_weighted_relu_mqa_scores`` times the key
+    scale):
+
+    ``logits[i, j] = sum_h w[i,h] * relu(q[i,h,:] . kv[j,:]) * kv_scale[j]`` for
+    ``ks[i] <= j < ke[i]``, -inf elsewhere (``clean_logits``; otherwise the
+    entries outside are left at 0 here, the reference leaves them unspecified).
+    q_fp8 uint8 [M, H, 128], kv_fp8 uint8 [N, 128], kv_scale f32 [N],
+    weights f32 [M, H]. float64 accumulation; returns f32 [M, N]."""
+    M, H, D = q_fp8.shape
+    N = kv_fp8.shape[0]
+    out = np.full((M, N), -np.inf if clean_logits else 0.0, dtype=np.float32)
+    qf = fp8_e4m3fn_decode(q_fp8).astype(np.float64)
+    kf = fp8_e4m3fn_decode(kv_fp8).astype(np.float64)
+    sc = np.asarray(kv_scale, dtype=np.float64)
+    w = np.asarray(weights, dtype=np.float64)
+    for i in range(M):
+        a, e = int(ks[i]), int(ke[i])
+        if e <= a:
+            continue
+        dots = qf[i] @ kf[a:e].T                                # [H, e-a]
+        out[i, a:e] = ((np.maximum(dots, 0.0) * w[i][:, None]).sum(axis=0) * sc[a:e]).astype(np.float32)
+    return out
