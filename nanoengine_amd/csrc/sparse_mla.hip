@@ -5,41 +5,42 @@
 //   o   = softmax(s) @ kv(idx)[:, :512],  lse = log(sum_i exp(s_i))
 // where kv(slot) is a 656-byte row [512 e4m3fn][4 x f32 tile scale][64 bf16].
 //
-// Workgroup = 4 waves = 64 heads of one token over one key split. The waves
-// form two pairs; a pair owns 32 heads and splits the work by dimension:
-// wave d of the pair contracts nope dims [256d, 256d+256) and rope dims
-// [32d, 32d+32) for the scores and produces output dims [256d, 256d+256).
-// Both halves of a score are summed through LDS, so each wave holds only its
-// half of the query (72 VGPRs) and of the output (128 accumulators).
+// Workgroup = 8 waves (two per SIMD) = 64 heads of one token over one key
+// split. Two waves share each SIMD so that one wave's matrix work overlaps the
+// other's vector work: a single wave issues a vector instruction only every
+// ~7 cycles, so at one wave per SIMD this kernel would be bound by vector
+// issue, not by the matrix cores. Each wave fits in 256 registers.
 //
-// Per block of 64 selected rows:
+// Wave w = (head half hp = w/4, quarter q = w%4); its 32 heads are
+// hp*32 + 0..31 of the workgroup's 64. Per block of 64 selected rows:
 //   gather : the raw 656-byte rows go straight from HBM into LDS with
 //            global_load_lds_dwordx4 - consecutive lanes take consecutive
-//            16-byte pieces of the packed rows, so each load instruction
-//            touches ~10 cache lines instead of 64 - into one of three
-//            buffers, two blocks ahead of use. The row indices themselves
-//            arrive the same way, four blocks ahead, in a five-entry ring.
-//            Invalid indices read a zero row. No registers hold data in
-//            flight, so the prefetch depth costs only LDS. An LDS-bound load
-//            holds its wave until the address unit has taken it (~50 cycles
-//            each), so a wave sends its loads in runs of four that share one
-//            M0 value, after the block's MFMAs.
-//   QK     : S^T[64 keys x 32 heads]. The nope part runs on
-//            v_mfma_scale_f32_32x32x64_f8f6f4: A = the raw fp8 rows straight
-//            from LDS with the row's tile scale as the E8M0 block scale (the
-//            cache's scales are powers of two, so this is exact); B = the
-//            query as two fp8 terms hi + lo with per-chunk E8M0 scales, which
-//            together hold each bf16 query value to ~2^-22 of its chunk's
-//            largest. The rope part (bf16 in the row) runs on
-//            v_mfma_f32_32x32x16_bf16 against the bf16 query.
-//   softmax: partner partials summed, online softmax in the exp2 domain with
-//            lazy rescaling (the running max moves only when a block raises
-//            it by more than 2^8).
-//   PV     : O[32 heads x 256] += P' . V on v_mfma_f32_32x32x16_bf16. V comes from the
-//            raw rows with ds_read_b64_tr_b8 (8 keys x 1 dim per lane, the
-//            B operand layout) and is converted with unit scale; the per-row
-//            tile scale is folded into P instead (P' = P * 2^k, exact), and
-//            P' comes straight from the score accumulators.
+//            16-byte pieces of the packed rows - into one of three buffers,
+//            two blocks ahead of use. The row indices arrive the same way,
+//            four blocks ahead, in a five-entry ring. Invalid indices read a
+//            zero row.
+//   QK     : wave (kh = q/2, d = q%2) forms the partial S^T[32 keys x 32
+//            heads] of keys 32kh..32kh+31 over nope dims [256d, 256d+256)
+//            and rope dims [32d, 32d+32). The nope part runs on
+//            v_mfma_scale_f32_32x32x64_f8f6f4: A = the raw fp8 rows from LDS
+//            with the row's tile scale as the E8M0 block scale (the cache's
+//            scales are powers of two, so this is exact); B = the query as two
+//            fp8 terms hi + lo with per-chunk E8M0 scales, which together hold
+//            each bf16 query value to ~2^-22 of its chunk's largest. The rope
+//            part (bf16 in the row) runs on v_mfma_f32_32x32x16_bf16.
+//   reduce : the two dim halves are summed by a reduce-scatter through LDS:
+//            wave (kh, d) ends with the full scores of keys 16o..16o+15,
+//            o = 2kh + d, so each score is exponentiated exactly once.
+//   softmax: per-head block maxima of the four key quarters are exchanged;
+//            online softmax in the exp2 domain with lazy rescaling (the
+//            running max moves only when a block raises it by more than 2^8).
+//            P goes to LDS once, as bf16.
+//   PV     : wave q produces output dims [128q, 128q+128) = V tile q of its
+//            32 heads: O += P' . V on v_mfma_f32_32x32x16_bf16, P' = P * 2^e
+//            with e the tile scale exponent of each key (a 16-bit add to the
+//            bf16 exponent field, read from a per-block table), V read from
+//            the raw rows with ds_read_b64_tr_b8 (8 keys x 1 dim per lane, the
+//            B operand layout) and converted with unit scale.
 // Splits over the key list (for small batches) write normalised partial
 // outputs and LSEs to a caller-provided workspace; a combine kernel merges
 // them with the LSE rule of merge_attention_states.
@@ -53,8 +54,10 @@ namespace dsa {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
-constexpr int kMlaThreads = 256;
+constexpr int kMlaThreads = 512;
+constexpr int kMlaWaves = kMlaThreads / 64;
 constexpr int kMlaHeadsPerWG = 64;
 constexpr int kMlaKeys = 64;              // rows per block
 constexpr int kMlaRowBytes = 656;
@@ -63,14 +66,21 @@ constexpr int kMlaDv = 512;
 constexpr int kBufBytes = kMlaKeys * kMlaRowBytes;    // 41984: one block of packed raw rows
 constexpr int kDmaPerBlock = kBufBytes / 1024;        // 41 wave-wide 16-byte loads per block
 constexpr int kNumBufs = 3;
-constexpr int kXchgOff = kNumBufs * kBufBytes;         // partial scores, 8 KB per wave
-constexpr int kSclOff = kXchgOff + 4 * 8192;           // per-wave row scales [2 tiles][64 keys]
-constexpr int kRingOff = kSclOff + 4 * 512;            // row indices, one 64-entry block per slot
+// LDS map (bytes)
+constexpr int kXsOff = kNumBufs * kBufBytes;          // score partials: [8 waves][64 lanes][8 f32]
+constexpr int kMxOff = kXsOff + kMlaWaves * 64 * 32;  // block maxima / final sums: [2 hp][32 heads][4 quarters] f32
+constexpr int kPOff = kMxOff + 2 * 32 * 4 * 4;        // P: [2 hp][4 quarters][64 lanes][8 bf16]
+constexpr int kEOff = kPOff + 2 * 4 * 64 * 16;        // exponent offsets: [4 tiles][4 k-steps][2 halves][8 u16]
+constexpr int kRingOff = kEOff + 4 * 4 * 2 * 16;      // row indices, one 64-entry block per slot
 constexpr int kRingSlots = 5;
-constexpr size_t kMlaSmemBytes = kRingOff + kRingSlots * 256;  // 162048
+constexpr size_t kMlaSmemBytes = kRingOff + kRingSlots * 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
+// Smallest P kept for a valid key (log2): P' = P * 2^e is formed by adding e to
+// the bf16 exponent field, which needs P to be a normal number.
+constexpr float kMinLogP = -60.0f;
+constexpr int kIdxWave = 7;                // the wave that fetches the row indices
 
 static_assert(kBufBytes % 1024 == 0, "a block of rows must be whole wave-wide loads");
 static_assert(kMlaSmemBytes <= 160 * 1024, "LDS budget");
@@ -107,10 +117,10 @@ __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
-// Wait until at most n of this wave's copies are outstanding (n in {0, 10, 11}).
+// Wait until at most n of this wave's copies are outstanding (n in {0, 5, 6}).
 __device__ __forceinline__ void wait_vm(int n) {
-  if (n >= 11) asm volatile("s_waitcnt vmcnt(11)" ::: "memory");
-  else if (n == 10) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  if (n >= 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else if (n == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 __device__ __forceinline__ void barrier() {
@@ -199,11 +209,16 @@ struct RowDma {
   bool on;
 };
 
-// Wave w sends loads [first(w), first(w) + count(w)) of the block: 11 for wave 0,
-// 10 for the others, in runs of four that share one M0 (LDS base) value.
-__device__ __forceinline__ int dma_count(int wave) { return kDmaPerBlock / 4 + (wave < kDmaPerBlock % 4 ? 1 : 0); }
-__device__ __forceinline__ int dma_first(int wave) { return wave * (kDmaPerBlock / 4) + min(wave, kDmaPerBlock % 4); }
-static_assert(kDmaPerBlock / 4 == 10 && kDmaPerBlock % 4 == 1, "wait_vm() counts 11 / 10 loads per wave");
+// Wave w sends loads [first(w), first(w) + count(w)) of the block's 41: six for
+// wave 0, five for the others, in runs that share one M0 (LDS base) value.
+__device__ __forceinline__ int dma_count(int wave) {
+  return kDmaPerBlock / kMlaWaves + (wave < kDmaPerBlock % kMlaWaves ? 1 : 0);
+}
+__device__ __forceinline__ int dma_first(int wave) {
+  return wave * (kDmaPerBlock / kMlaWaves) + min(wave, kDmaPerBlock % kMlaWaves);
+}
+static_assert(kDmaPerBlock / kMlaWaves == 5 && kDmaPerBlock % kMlaWaves == 1,
+              "wait_vm() counts 6 / 5 loads per wave");
 
 __device__ __forceinline__ uint64_t row_dma_addr(const RowDma& g, int i) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -233,7 +248,7 @@ __device__ __forceinline__ void prep_rows(RowDma& g, const MlaParams& P, const u
   }
   g.lbuf = __builtin_amdgcn_readfirstlane(lds_addr(buf));
   // an opaque lane id keeps the per-load lane offsets from being hoisted out
-  // of the block loop, where they would pin ~30 VGPRs for the whole kernel
+  // of the block loop, where they would pin registers for the whole kernel
   g.ln = lane;
   asm volatile("" : "+v"(g.ln));
 }
@@ -243,29 +258,29 @@ __device__ __forceinline__ void prep_rows(RowDma& g, const MlaParams& P, const u
 __device__ __forceinline__ void issue_run(const RowDma& g, int i, int n, int wave) {
   if (!g.on) return;
   const uint32_t m0 = g.lbuf + 1024 * (dma_first(wave) + i);
-  const uint64_t a0 = row_dma_addr(g, i);
-  const uint64_t a1 = row_dma_addr(g, i + 1) - 1024;
-  const uint64_t a2 = row_dma_addr(g, i + 2) - 2048;
-  const uint64_t a3 = row_dma_addr(g, i + 3) - 3072;
   const uint32_t m = __builtin_amdgcn_readfirstlane(m0);
-  if (n == 4)
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024\n\t"
-                 "global_load_lds_dwordx4 %2, off offset:2048\n\tglobal_load_lds_dwordx4 %3, off offset:3072"
-                 ::"v"(a0), "v"(a1), "v"(a2), "v"(a3), "{m0}"(m) : "memory");
-  else if (n == 3)
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024\n\t"
-                 "global_load_lds_dwordx4 %2, off offset:2048"
-                 ::"v"(a0), "v"(a1), "v"(a2), "{m0}"(m) : "memory");
-  else if (n == 2)
+  const uint64_t a0 = row_dma_addr(g, i);
+  if (n == 1) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(a0), "{m0}"(m) : "memory");
+    return;
+  }
+  const uint64_t a1 = row_dma_addr(g, i + 1) - 1024;
+  if (n == 2) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024"
                  ::"v"(a0), "v"(a1), "{m0}"(m) : "memory");
+    return;
+  }
+  const uint64_t a2 = row_dma_addr(g, i + 2) - 2048;
+  const uint64_t a3 = row_dma_addr(g, i + 3) - 3072;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024\n\t"
+               "global_load_lds_dwordx4 %2, off offset:2048\n\tglobal_load_lds_dwordx4 %3, off offset:3072"
+               ::"v"(a0), "v"(a1), "v"(a2), "v"(a3), "{m0}"(m) : "memory");
 }
 
-// All of this wave's loads of the block: 4 + 4 + 3 (wave 0) or 4 + 4 + 2.
+// All of this wave's loads of the block: 4 + 2 (wave 0) or 4 + 1.
 __device__ __forceinline__ void issue_all(const RowDma& g, int wave) {
   issue_run(g, 0, 4, wave);
-  issue_run(g, 4, 4, wave);
-  issue_run(g, 8, dma_count(wave) - 8, wave);
+  issue_run(g, 4, dma_count(wave) - 4, wave);
 }
 
 __device__ __forceinline__ void issue_rows(const MlaParams& P, const uint8_t* smem, int j, uint8_t* buf,
@@ -281,13 +296,17 @@ __device__ __forceinline__ void issue_index(const MlaParams& P, uint8_t* smem, i
   dma4(src, __builtin_amdgcn_readfirstlane(lds_addr(smem + kRingOff + (j % kRingSlots) * 256)));
 }
 
-__global__ void __launch_bounds__(kMlaThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(kMlaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 sparse_mla_kernel(const MlaParams P) {
   extern __shared__ __align__(16) uint8_t smem[];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5, c32 = lane & 31;
-  const int pair = wave >> 1, d = wave & 1;
+  const int hp = wave >> 2, q4 = wave & 3;
+  const int kh = q4 >> 1, d = q4 & 1;  // QK: key half, dim half
+  const int o4 = 2 * kh + d;           // owned key quarter after the reduce-scatter
+  const int jt = q4;                   // PV: V tile (output dims [128 jt, 128 jt + 128))
 
   // XCD-aware order: consecutive logical work items (the head groups and
   // splits of one token) land on the same XCD and share its L2.
@@ -303,8 +322,8 @@ sparse_mla_kernel(const MlaParams P) {
   const int key_begin = split * chunk;
   const int nblk = chunk / kMlaKeys;
 
-  const int h_pair = hg * kMlaHeadsPerWG + pair * 32;  // first head of the pair
-  const int head = h_pair + c32;                       // this lane's head (score columns)
+  const int h_half = hg * kMlaHeadsPerWG + hp * 32;  // first head of this wave's 32
+  const int head = h_half + c32;                     // this lane's head (score columns)
   const bool head_ok = head < P.H;
 
   // Query B operands. Nope chunk c (dims 256d + 64c + 32h + 0..31 for lane half
@@ -371,17 +390,17 @@ sparse_mla_kernel(const MlaParams P) {
   // compiler's wait bookkeeping.) 0x0f70 = vmcnt(0) only.
   __builtin_amdgcn_s_waitcnt(0x0f70);
 
-  v16f o[8];
+  v16f o[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
-  float m_run = -__builtin_inff();  // per head c32, log2 domain
-  float l_run = 0.f;                // per head c32, this lane half's keys only
+  float m_run = -__builtin_inff();  // per head c32, log2 domain (identical in the 4 waves of a head half)
+  float l_run = 0.f;                // per head c32: this lane's 8 keys of each block only
 
   const int my_dma = dma_count(wave);
   // prologue: indices of blocks 0-3, then rows of blocks 0 and 1
-  if (wave == 1) {
+  if (wave == kIdxWave) {
     for (int j = 0; j < 4 && j < nblk; ++j) issue_index(P, smem, t, key_begin, j, lane);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
@@ -389,170 +408,153 @@ sparse_mla_kernel(const MlaParams P) {
   issue_rows(P, smem, 0, smem, lane, wave);
   if (nblk > 1) issue_rows(P, smem, 1, smem + kBufBytes, lane, wave);
 
-  float* xmine = reinterpret_cast<float*>(smem + kXchgOff + wave * 8192);
-  const float* xpart = reinterpret_cast<const float*>(smem + kXchgOff + (wave ^ 1) * 8192);
-  float* scl = reinterpret_cast<float*>(smem + kSclOff + wave * 512);
+  float* xs_mine = reinterpret_cast<float*>(smem + kXsOff) + (wave * 64 + lane) * 8;
+  const float* xs_part = reinterpret_cast<const float*>(smem + kXsOff) + ((wave ^ 1) * 64 + lane) * 8;
+  float* mx = reinterpret_cast<float*>(smem + kMxOff) + (hp * 32 + c32) * 4;
+  uint8_t* pbuf = smem + kPOff + hp * 4 * 1024;
+  uint16_t* etab = reinterpret_cast<uint16_t*>(smem + kEOff);
 
   for (int n = 0; n < nblk; ++n) {
-    // rows of block n (and, for wave 1, the indices of block n+2) have landed
+    // B0: rows of block n (and, for the index wave, the indices of block n+2) have landed
     int allow = n + 1 < nblk ? my_dma : 0;
-    if (wave == 1 && n >= 1 && n + 3 < nblk) allow += 1;
+    if (wave == kIdxWave && n >= 1 && n + 3 < nblk) allow += 1;
     wait_vm(allow);
     barrier();
     const uint8_t* buf = smem + (n % kNumBufs) * kBufBytes;
     const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kRingOff + (n % kRingSlots) * 256)[lane];
     const uint64_t vmask = __ballot(slot_n >= 0);
-    if (wave == 1 && n + 4 < nblk) issue_index(P, smem, t, key_begin, n + 4, lane);
-    // block n+2's rows go out between this block's MFMAs (loads 0-3 in QK, 4-10 in PV)
-    RowDma g;
-    prep_rows(g, P, smem, n + 2, smem + ((n + 2) % kNumBufs) * kBufBytes, lane, n + 2 < nblk);
+    if (wave == kIdxWave && n + 4 < nblk) issue_index(P, smem, t, key_begin, n + 4, lane);
 
-    // ---- partial S^T over this wave's dims: s[kt][r] = key 32kt + 8(r/4) + 4h + r%4, head c32
-    v16f s[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
-    v2f ksc[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-      ksc[kt] = *reinterpret_cast<const v2f*>(buf + (32 * kt + c32) * kMlaRowBytes + 512 + 8 * d);
-    // E8M0 of the row's tile scales (powers of two): byte tt = tile 2d + tt
-    int ke[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-      ke[kt] = (int)(((__float_as_uint(ksc[kt][0]) >> 23) & 0xffu) | (((__float_as_uint(ksc[kt][1]) >> 23) & 0xffu) << 8));
-    // K chunk c: lane half h holds bytes 256d + 64c + 32h .. +32 of key 32kt + c32
-    const uint8_t* krow = buf + c32 * kMlaRowBytes + 256 * d + 32 * h;
-    v8i kraw[2][2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) kraw[0][kt] = lds_read32(krow + 32 * kt * kMlaRowBytes);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c + 1 < 4) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) kraw[(c + 1) & 1][kt] = lds_read32(krow + 32 * kt * kMlaRowBytes + 64 * (c + 1));
-      }
-      // alternate the two accumulators so that no MFMA waits on its predecessor
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma_fp8_chunk(c, kraw[c & 1][kt], qhi[c], s[kt], ke[kt], qe_hi);
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma_fp8_chunk(c, kraw[c & 1][kt], qlo[c], s[kt], ke[kt], qe_lo);
-      __builtin_amdgcn_sched_barrier(0);
+    // Exponent table of this block: entry (tile, key) = the tile scale's
+    // exponent shifted into the bf16 exponent field, at the position the PV
+    // A operand holds that key (k-step key/16, lane half (key/4)%2, element
+    // 4((key/8)%2) + key%4).
+    if (wave < 4) {
+      const int key = lane, tile = wave;
+      const uint32_t sb = *reinterpret_cast<const uint32_t*>(buf + key * kMlaRowBytes + 512 + 4 * tile);
+      const int e = (int)((sb >> 23) & 0xffu) - 127;
+      const int pos = ((tile * 4 + (key >> 4)) * 2 + ((key >> 2) & 1)) * 8 + 4 * ((key >> 3) & 1) + (key & 3);
+      etab[pos] = (uint16_t)((uint32_t)(e << 7) & 0xffffu);
     }
+
+    // ---- partial S^T[32 keys x 32 heads] over this wave's dims:
+    // s[r] = key 32kh + 8(r/4) + 4h + r%4, head c32
+    v16f s;
 #pragma unroll
-    for (int rho = 0; rho < 2; ++rho)
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+    {
+      const uint8_t* row = buf + (32 * kh + c32) * kMlaRowBytes;
+      const v2f ksc = *reinterpret_cast<const v2f*>(row + 512 + 8 * d);
+      // E8M0 of the row's tile scales (powers of two): byte tt = tile 2d + tt
+      const int ke = (int)(((__float_as_uint(ksc[0]) >> 23) & 0xffu) | (((__float_as_uint(ksc[1]) >> 23) & 0xffu) << 8));
+      // K chunk c: lane half h holds bytes 256d + 64c + 32h .. +32 of key 32kh + c32
+      const uint8_t* krow = row + 256 * d + 32 * h;
+      v8i kraw[2];
+      kraw[0] = lds_read32(krow);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const v4i rope = *reinterpret_cast<const v4i*>(buf + (32 * kt + c32) * kMlaRowBytes + 528 + 64 * d +
-                                                       32 * rho + 16 * h);
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(rope), as_v8bf(qr[rho]), s[kt], 0, 0, 0);
+      for (int c = 0; c < 4; ++c) {
+        if (c + 1 < 4) kraw[(c + 1) & 1] = lds_read32(krow + 64 * (c + 1));
+        s = mfma_fp8_chunk(c, kraw[c & 1], qhi[c], s, ke, qe_hi);
+        s = mfma_fp8_chunk(c, kraw[c & 1], qlo[c], s, ke, qe_lo);
       }
-    // this wave's row scales, by key, for folding into P
-    if (h == 0) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        scl[32 * kt + c32] = ksc[kt][0];
-        scl[64 + 32 * kt + c32] = ksc[kt][1];
+      for (int rho = 0; rho < 2; ++rho) {
+        const v4i rope = *reinterpret_cast<const v4i*>(row + 528 + 64 * d + 32 * rho + 16 * h);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(rope), as_v8bf(qr[rho]), s, 0, 0, 0);
       }
     }
 
-    // ---- exchange partial scores with the partner wave
+    // ---- reduce-scatter with the dim partner (wave ^ 1): this wave keeps
+    // s[8d .. 8d+7] = keys 16 o4 + 8(i/4) + 4h + i%4 (i = 0..7) and sends the rest.
+    float sv[8];
+    if (d == 0) {
+      *reinterpret_cast<v4f*>(xs_mine) = v4f{s[8], s[9], s[10], s[11]};
+      *reinterpret_cast<v4f*>(xs_mine + 4) = v4f{s[12], s[13], s[14], s[15]};
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const v4f v = {s[q >> 2][4 * (q & 3)], s[q >> 2][4 * (q & 3) + 1], s[q >> 2][4 * (q & 3) + 2],
-                     s[q >> 2][4 * (q & 3) + 3]};
-      *reinterpret_cast<v4f*>(xmine + q * 256 + lane * 4) = v;
+      for (int i = 0; i < 8; ++i) sv[i] = s[i];
+    } else {
+      *reinterpret_cast<v4f*>(xs_mine) = v4f{s[0], s[1], s[2], s[3]};
+      *reinterpret_cast<v4f*>(xs_mine + 4) = v4f{s[4], s[5], s[6], s[7]};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = s[8 + i];
     }
-    barrier();
+    barrier();  // B1
+    {
+      const v4f a = *reinterpret_cast<const v4f*>(xs_part);
+      const v4f b = *reinterpret_cast<const v4f*>(xs_part + 4);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const v4f v = *reinterpret_cast<const v4f*>(xpart + q * 256 + lane * 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) s[q >> 2][4 * (q & 3) + e] += v[e];
+      for (int i = 0; i < 4; ++i) {
+        sv[i] += a[i];
+        sv[4 + i] += b[i];
+      }
     }
-
-    // ---- online softmax (exp2 domain), lazy rescale
-    float mloc = -__builtin_inff();
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kt][r] *= P.scale_log2;
+    // invalid keys score -inf (their rows are zeros, so P' . V gets exact zeros)
+    const uint64_t vm = vmask >> (16 * o4 + 4 * h);
     if (vmask != ~0ull) {
-      // invalid keys score -inf; their rows are zeros, so P . V gets exact zeros
-      const uint64_t vm = vmask >> (4 * h);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (!((vm >> (32 * kt + 8 * (r >> 2) + (r & 3))) & 1ull)) s[kt][r] = -__builtin_inff();
+      for (int i = 0; i < 8; ++i)
+        if (!((vm >> (8 * (i >> 2) + (i & 3))) & 1ull)) sv[i] = -__builtin_inff();
     }
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kt][r]);
+    float mloc = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
     mloc = fmaxf(mloc, shfl_xor(mloc, 32));
-    const bool need = mloc > m_run + kRescaleThreshold;  // true on the first valid block
-    if (__ballot(need)) {
-      const float m_new = need ? mloc : m_run;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
-      l_run *= alpha;
-      m_run = m_new;
-      // o rows are heads 8(r/4) + 4h + r%4
-      int hh = 4 * h;
-      asm volatile("" : "+v"(hh));
-      float ar[16];
+    if (h == 0) mx[o4] = mloc;
+    barrier();  // B2
+
+    // ---- online softmax (exp2 domain), lazy rescale; the block maximum is
+    // the same in the four waves of a head half, so are m_run and alpha
+    {
+      const v4f m4 = *reinterpret_cast<const v4f*>(mx);
+      const float mblk = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])) * P.scale_log2;
+      const bool need = mblk > m_run + kRescaleThreshold;  // true on the first valid block
+      if (__ballot(need)) {
+        const float m_new = need ? mblk : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
+        l_run *= alpha;
+        m_run = m_new;
+        // o rows are heads 8(r/4) + 4h + r%4
+        int hh = 4 * h;
+        asm volatile("" : "+v"(hh));
+        float ar[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ar[r] = __shfl(alpha, 8 * (r >> 2) + hh + (r & 3), 64);
-      // one output tile at a time: the accumulators live in AGPRs
+        for (int r = 0; r < 16; ++r) ar[r] = __shfl(alpha, 8 * (r >> 2) + hh + (r & 3), 64);
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
+        for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[nt][r] *= ar[r];
-        __builtin_amdgcn_sched_barrier(0);
+          for (int r = 0; r < 16; ++r) o[nt][r] *= ar[r];
       }
     }
     // m_run is -inf only while every key so far was invalid; then p = 0
     const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
-    float psum = 0.f;
+    float pv[8];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int i = 0; i < 8; ++i)
+      pv[i] = __builtin_amdgcn_exp2f(fmaxf(fmaf(sv[i], P.scale_log2, -m_use), kMinLogP));
+    if (vmask != ~0ull) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(s[kt][r] - m_use);
-        s[kt][r] = pv;
-        psum += pv;
-      }
-    l_run += psum;
+      for (int i = 0; i < 8; ++i)
+        if (!((vm >> (8 * (i >> 2) + (i & 3))) & 1ull)) pv[i] = 0.f;
+    }
+    l_run += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+    {
+      const v4i pw = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]), cvt_pk_bf16(pv[4], pv[5]),
+                      cvt_pk_bf16(pv[6], pv[7])};
+      *reinterpret_cast<v4i*>(pbuf + (o4 * 64 + lane) * 16) = pw;
+    }
+    barrier();  // B3
 
-    // ---- O += P' . V. Lane (group G = lane/16, m = lane%16) addresses key row
-    // 8(e/4) + 4h + e%4 (e = m/2) and dims (G%2)*16 + 8(m%2) of each 32-dim tile.
-    const int m16 = lane & 15, G = lane >> 4;
-    const int e8 = m16 >> 1;
-    const uint8_t* vb = buf + (8 * (e8 >> 2) + 4 * h + (e8 & 3)) * kMlaRowBytes + 256 * d + (G & 1) * 16 +
-                        8 * (m16 & 1);
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      // P' for row-scale tile 2d + tt: element e of k-step (kt, j) is key 32kt + 16j + 8(e/4) + 4h + e%4
-      v4i pa[2][2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v4f sa = *reinterpret_cast<const v4f*>(scl + 64 * tt + 32 * kt + 16 * j + 4 * h);
-          const v4f sb = *reinterpret_cast<const v4f*>(scl + 64 * tt + 32 * kt + 16 * j + 8 + 4 * h);
-          pa[kt][j][0] = cvt_pk_bf16(s[kt][8 * j + 0] * sa[0], s[kt][8 * j + 1] * sa[1]);
-          pa[kt][j][1] = cvt_pk_bf16(s[kt][8 * j + 2] * sa[2], s[kt][8 * j + 3] * sa[3]);
-          pa[kt][j][2] = cvt_pk_bf16(s[kt][8 * j + 4] * sb[0], s[kt][8 * j + 5] * sb[1]);
-          pa[kt][j][3] = cvt_pk_bf16(s[kt][8 * j + 6] * sb[2], s[kt][8 * j + 7] * sb[3]);
-        }
+    // ---- O[32 heads x 128 dims] += P' . V over the block's 64 keys (four k-steps of 16).
+    // Lane (group G = lane/16, m = lane%16) addresses key row 8(e/4) + 4h + e%4
+    // (e = m/2) and dims (G%2)*16 + 8(m%2) of each 32-dim tile.
+    {
+      const int m16 = lane & 15, G = lane >> 4;
+      const int e8 = m16 >> 1;
+      const uint8_t* vb = buf + (8 * (e8 >> 2) + 4 * h + (e8 & 3)) * kMlaRowBytes + 128 * jt + (G & 1) * 16 +
+                          8 * (m16 & 1);
       // The transposing reads take no immediate offset, so each address is
-      // formed from an opaque base right before use; otherwise all 32 would be
-      // hoisted out of the block loop into registers.
-      // k-step outer, output tile inner: the four MFMAs of a k-step go to four
-      // different accumulators, so none waits for the previous one's result.
+      // formed from an opaque base right before use; otherwise all of them
+      // would be hoisted out of the block loop into registers.
       auto vstep = [&](int ks) {
-        uint32_t a = lds_addr(vb) + (16 * ks) * kMlaRowBytes + 32 * (4 * tt);
+        uint32_t a = lds_addr(vb) + (16 * ks) * kMlaRowBytes;
         asm volatile("" : "+v"(a));
         return a;
       };
@@ -569,54 +571,72 @@ sparse_mla_kernel(const MlaParams P) {
 #pragma unroll
           for (int nn = 0; nn < 4; ++nn) vr[(ks + 1) & 1][nn] = lds_read_tr8_at(p + 32 * nn);
         }
+        const v4i pr = *reinterpret_cast<const v4i*>(pbuf + (ks * 64 + lane) * 16);
+        const v4i ev = *reinterpret_cast<const v4i*>(etab + ((jt * 4 + ks) * 2 + h) * 8);
+        v4i pa;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // (bit_cast of a vector element reads element 0; copy to scalars first)
+          const int pe = pr[e], ee = ev[e];
+          pa[e] = __builtin_bit_cast(int, __builtin_bit_cast(v2u16, pe) + __builtin_bit_cast(v2u16, ee));
+        }
         v8bf vb16[4];
 #pragma unroll
         for (int nn = 0; nn < 4; ++nn) vb16[nn] = fp8x8_to_bf16(vr[ks & 1][nn]);
 #pragma unroll
         for (int nn = 0; nn < 4; ++nn)
-          o[4 * tt + nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa[ks >> 1][ks & 1]), vb16[nn],
-                                                                   o[4 * tt + nn], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
+          o[nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa), vb16[nn], o[nn], 0, 0, 0);
       }
     }
-    // block n+2's rows: an LDS-bound copy holds its wave until the address
-    // unit has taken it, so all of them go out after this block's MFMAs
-    issue_all(g, wave);
+    // block n+2's rows, into the buffer of block n-1 that every wave left at B0
+    {
+      RowDma g;
+      prep_rows(g, P, smem, n + 2, smem + ((n + 2) % kNumBufs) * kBufBytes, lane, n + 2 < nblk);
+      issue_all(g, wave);
+    }
   }
 
   // drain: nothing may be left in flight when the workgroup ends
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (h_pair >= P.H) return;
+  // total of P per head: both lane halves, then the four key quarters
   l_run += shfl_xor(l_run, 32);
+  barrier();
+  if (h == 0) mx[o4] = l_run;
+  barrier();
+  {
+    const v4f l4 = *reinterpret_cast<const v4f*>(mx);
+    l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
+  }
+  if (h_half >= P.H) return;
   const bool any = l_run > 0.f;
   const float inv = any ? 1.f / l_run : 0.f;
   const float lse = any ? (m_run + __builtin_amdgcn_logf(l_run)) * kLn2 : -__builtin_inff();
-  // o[nt][r]: head h_pair + 8(r/4) + 4h + r%4, dim 256d + 32nt + c32
+  // o[nt][r]: head h_half + 8(r/4) + 4h + r%4, dim 128 jt + 32nt + c32
   if (P.splits == 1) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
       const float ir = __shfl(inv, hr, 64);
-      if (h_pair + hr < P.H) {
-        uint16_t* orow = P.out + ((int64_t)t * P.H + h_pair + hr) * kMlaDv + 256 * d + c32;
+      if (h_half + hr < P.H) {
+        uint16_t* orow = P.out + ((int64_t)t * P.H + h_half + hr) * kMlaDv + 128 * jt + c32;
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
+        for (int nt = 0; nt < 4; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
       }
     }
-    if (h == 0 && d == 0 && head_ok && P.lse) P.lse[(int64_t)t * P.H + head] = lse;
+    if (h == 0 && jt == 0 && head_ok && P.lse) P.lse[(int64_t)t * P.H + head] = lse;
   } else {
-    const int64_t row0 = ((int64_t)split * P.T + t) * P.H + h_pair;
+    const int64_t row0 = ((int64_t)split * P.T + t) * P.H + h_half;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
       const float ir = __shfl(inv, hr, 64);
-      if (h_pair + hr < P.H) {
-        float* orow = P.ws_o + (row0 + hr) * kMlaDv + 256 * d + c32;
+      if (h_half + hr < P.H) {
+        float* orow = P.ws_o + (row0 + hr) * kMlaDv + 128 * jt + c32;
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) orow[32 * nt] = o[nt][r] * ir;
+        for (int nt = 0; nt < 4; ++nt) orow[32 * nt] = o[nt][r] * ir;
       }
     }
-    if (h == 0 && d == 0 && head_ok) P.ws_lse[row0 + c32] = lse;
+    if (h == 0 && jt == 0 && head_ok) P.ws_lse[row0 + c32] = lse;
   }
 }
 
