@@ -290,6 +290,23 @@ DSA_API int dsa_mqa_logits(const uint8_t* q, const uint8_t* kv, const float* kv_
                            float* logits, int64_t logits_stride, int64_t num_cols,
                            int clean_logits, void* stream);
 
+
+/* Paged indexer cache -> contiguous ragged keys and scales (prefill indexer).
+ *   cache        [pages, page_bytes] uint8, page = [page_size x 128 fp8][page_size x f32]
+ *   block_table  [num_seqs, *] int32, row stride bt_stride
+ *   cu_seqlens_k [num_seqs + 1] int32 (int64 when cu_is_64), cu[0] = 0, cu[num_seqs] = total_k
+ *   key_out      [total_k, 128] uint8;  scale_out [total_k, 4] uint8 (the f32 scale bytes)
+ * Ragged token cu[b] + i is token i of sequence b: page block_table[b, i / page_size],
+ * row i % page_size. head_dim must be 128.
+ * Replaces gather_indexer_cache(cache, block_table, cu_seqlens_k, page_size=, head_dim=,
+ * total_k=, max_seqlen_k=) (dlengine/runtime/kernel/triton/generic/indexer_cache_gather.py:60-114,
+ * called at dlengine/runtime/layers/backends/dsa/indexer/lightning.py:1180-1188). */
+DSA_API int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, int page_size,
+                                     int head_dim, const int32_t* block_table, int64_t bt_stride,
+                                     const void* cu_seqlens_k, int cu_is_64, int num_seqs,
+                                     int64_t total_k, uint8_t* key_out, uint8_t* scale_out,
+                                     void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

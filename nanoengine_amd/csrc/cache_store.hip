@@ -73,6 +73,37 @@ indexer_k_store_kernel(const uint16_t* __restrict__ k, int64_t row_stride, const
   if (lane == 0) reinterpret_cast<float*>(base + (int64_t)page_size * 128)[off] = sf;
 }
 
+
+// Paged split-layout indexer cache -> contiguous ragged keys and scales
+// (dlengine/runtime/kernel/triton/generic/indexer_cache_gather.py:8-114).
+// Ragged token cu[b] + i is token i of sequence b, read through block_table[b].
+// Eight lanes copy one token's 128 key bytes (16 B each); the first of them
+// also copies its 4-byte scale. The sequence of a token is found by binary
+// search over cu_seqlens_k.
+__global__ void __launch_bounds__(256)
+gather_indexer_cache_kernel(const uint8_t* __restrict__ cache, int64_t page_bytes, int page_size,
+                            const int32_t* __restrict__ block_table, int64_t bt_stride,
+                            const void* __restrict__ cu, int cu_is_64, int num_seqs, int64_t total_k,
+                            uint8_t* __restrict__ key_out, uint8_t* __restrict__ scale_out) {
+  const int64_t tok = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int piece = threadIdx.x & 7;
+  if (tok >= total_k) return;
+  int lo = 0, hi = num_seqs;  // largest b with cu[b] <= tok
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (load_slot(cu, cu_is_64, mid) <= tok) lo = mid; else hi = mid;
+  }
+  const int64_t i = tok - load_slot(cu, cu_is_64, lo);
+  const int64_t page = block_table[(int64_t)lo * bt_stride + i / page_size];
+  const int64_t off = i % page_size;
+  const uint8_t* base = cache + page * page_bytes;
+  *reinterpret_cast<v4i*>(key_out + tok * 128 + 16 * piece) =
+      *reinterpret_cast<const v4i*>(base + off * 128 + 16 * piece);
+  if (piece == 0)
+    *reinterpret_cast<uint32_t*>(scale_out + tok * 4) =
+        *reinterpret_cast<const uint32_t*>(base + (int64_t)page_size * 128 + off * 4);
+}
+
 }  // namespace dsa
 
 extern "C" {
@@ -104,6 +135,29 @@ int dsa_indexer_k_store(const void* k, int64_t k_row_stride, const void* slots, 
   hipLaunchKernelGGL(indexer_k_store_kernel, dim3((num_tokens + 3) / 4), dim3(256), 0, (hipStream_t)stream,
                      static_cast<const uint16_t*>(k), k_row_stride, slots, slot_is_64, num_tokens, cache, page_size);
   return check_launch("dsa_indexer_k_store");
+}
+
+
+int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, int page_size, int head_dim,
+                             const int32_t* block_table, int64_t bt_stride, const void* cu_seqlens_k,
+                             int cu_is_64, int num_seqs, int64_t total_k, uint8_t* key_out,
+                             uint8_t* scale_out, void* stream) {
+  using namespace dsa;
+  if (head_dim != 128)
+    return set_error(kUnsupported, "dsa_gather_indexer_cache: head_dim=%d (only 128 is supported)", head_dim);
+  if (page_size <= 0 || num_seqs < 0 || total_k < 0 || page_bytes < (int64_t)page_size * 132)
+    return set_error(kInvalidArgument, "dsa_gather_indexer_cache: bad sizes");
+  if (total_k == 0) return kOk;
+  if (!cache || !block_table || !cu_seqlens_k || !key_out || !scale_out || num_seqs == 0)
+    return set_error(kInvalidArgument, "dsa_gather_indexer_cache: null pointer or no sequences");
+  if (((reinterpret_cast<uintptr_t>(cache) | reinterpret_cast<uintptr_t>(key_out)) & 15) || (page_bytes & 15) ||
+      (reinterpret_cast<uintptr_t>(scale_out) & 3))
+    return set_error(kInvalidArgument, "dsa_gather_indexer_cache: cache and keys must be 16-byte aligned");
+  const int64_t nwg = (total_k + 31) / 32;
+  hipLaunchKernelGGL(gather_indexer_cache_kernel, dim3((unsigned)nwg), dim3(256), 0, (hipStream_t)stream, cache,
+                     page_bytes, page_size, block_table, bt_stride, cu_seqlens_k, cu_is_64, num_seqs, total_k,
+                     key_out, scale_out);
+  return check_launch("dsa_gather_indexer_cache");
 }
 
 }  // extern "C"

@@ -1,4 +1,4 @@
-"""Decode-time lightning-indexer selection on MI355X.
+"""Lightning-indexer selection on MI355X: decode and chunked prefill.
 
 Mirrors the selection half of ``Indexer.forward``
 (dlengine/runtime/layers/backends/dsa/indexer/lightning.py:1357-1492): paged
@@ -11,6 +11,8 @@ from __future__ import annotations
 import torch
 
 from . import deep_gemm, deepseek_v4, ops
+from .deepseek_v4 import topk_transform_ragged
+from .indexer_cache_gather import gather_indexer_cache
 
 INDEXER_QUANT_BLOCK_SIZE = 128
 
@@ -119,3 +121,107 @@ def indexer_decode_topk(q_fp8: torch.Tensor, weights: torch.Tensor, kv_cache_buf
 def _logits_into(q4, kv_cache, weights, ctx, bt, max_context_len, out):
     kv = kv_cache.reshape(kv_cache.shape[0], -1)
     return ops.indexer_logits(q4, kv, weights, ctx, bt, max_context_len, out=out)
+
+
+def _prefill_mqa_chunk_rows(num_queries: int, num_keys: int, device: torch.device,
+                            max_rows: int | None = None) -> int:
+    """Query rows per ragged-logits chunk, from the memory a [rows, num_keys]
+    f32 logits tensor needs (lightning.py:381-405)."""
+    if num_queries <= 0:
+        return 0
+    if num_keys <= 0:
+        raise ValueError("prefill Indexer requires at least one key")
+    if max_rows is not None and max_rows <= 0:
+        raise ValueError(f"max_rows must be positive, got {max_rows}")
+    rows = num_queries
+    logits_elements = num_queries * num_keys
+    if logits_elements >= 8_000_000:
+        free_mem, total_mem = torch.cuda.mem_get_info(device)
+        logits_bytes = logits_elements * 4
+        if logits_bytes * 2 > free_mem or logits_bytes > total_mem * 0.3:
+            bytes_per_row = num_keys * 4
+            rows = max(1, int((free_mem * 0.45) // bytes_per_row))
+    if max_rows is not None:
+        rows = min(rows, max_rows)
+    return min(rows, num_queries)
+
+
+def compute_prefill_topk_paged(q_fp8: torch.Tensor, weights: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                               cu_seqlens_k: torch.Tensor, block_table: torch.Tensor,
+                               cache_buf: torch.Tensor, *, page_size: int = 64, index_topk: int = 2048,
+                               query_chunk: int | None = None) -> torch.Tensor:
+    """Prefill top-k with ragged fp8 MQA logits: the selection half of
+    ``Indexer.compute_prefill_topk_paged`` (lightning.py:1081-1250), from the
+    quantised queries on.
+
+    q_fp8 [num_queries, 64, 128] float8_e4m3fn and weights [num_queries, 64]
+    f32 (the q prologue's outputs); cu_seqlens_q / cu_seqlens_k [num_seqs + 1]
+    (each sequence's fresh queries are the last q_len of its k_len keys, whose
+    keys are already in the paged cache); block_table [num_seqs, pages] int32;
+    cache_buf [num_pages, page_size * 132] uint8. Returns packed global
+    logical indices [num_queries, index_topk] int32 into the ragged key order
+    (sequence b's keys at cu_seqlens_k[b] ...), -1 padded.
+    """
+    if query_chunk is not None and query_chunk <= 0:
+        raise ValueError(f"query_chunk must be positive, got {query_chunk}")
+    if cu_seqlens_q.shape != cu_seqlens_k.shape:
+        raise RuntimeError("cu_seqlens_q/cu_seqlens_k shape mismatch: "
+                           f"{cu_seqlens_q.shape} vs {cu_seqlens_k.shape}")
+    num_queries = q_fp8.shape[0]
+    indices = torch.full((num_queries, index_topk), -1, dtype=torch.int32, device=q_fp8.device)
+    if num_queries == 0:
+        return indices
+    head_dim = q_fp8.shape[-1]
+    num_seqs = cu_seqlens_q.numel() - 1
+    if block_table.shape[0] != num_seqs:
+        raise RuntimeError(f"block_table/cu_seqlens batch mismatch: {block_table.shape[0]} vs {num_seqs}")
+    q_first = int(cu_seqlens_q[0].item())
+    k_first = int(cu_seqlens_k[0].item())
+    q_total = int(cu_seqlens_q[-1].item())
+    if q_first != 0 or k_first != 0:
+        raise RuntimeError("ragged Indexer cu_seqlens must start at zero")
+    if q_total != num_queries:
+        raise RuntimeError(f"cu_seqlens_q does not cover the packed queries: {q_total} vs {num_queries}")
+    q_lens = (cu_seqlens_q[1:] - cu_seqlens_q[:-1]).to(torch.int32)
+    k_lens = (cu_seqlens_k[1:] - cu_seqlens_k[:-1]).to(torch.int32)
+    if bool(torch.any(q_lens < 0).item()) or bool(torch.any(k_lens < q_lens).item()):
+        raise RuntimeError("Invalid prefill ragged lengths: K length must cover every Q length")
+    used_pages = torch.div(k_lens + page_size - 1, page_size, rounding_mode="floor")
+    if int(used_pages.max().item()) > block_table.shape[1]:
+        raise RuntimeError("Indexer block table is too short for the longest sequence")
+
+    total_k = int(cu_seqlens_k[-1].item())
+    max_seqlen_k = int(k_lens.max().item())
+    key_bytes, scale_bytes = gather_indexer_cache(cache_buf, block_table, cu_seqlens_k, page_size=page_size,
+                                                  head_dim=head_dim, total_k=total_k, max_seqlen_k=max_seqlen_k)
+    kv_fp8 = (key_bytes.view(torch.float8_e4m3fn), scale_bytes.view(torch.float32).reshape(-1))
+
+    q_to_seq = torch.repeat_interleave(torch.arange(num_seqs, dtype=torch.int64, device=q_fp8.device),
+                                       q_lens.to(torch.int64), output_size=num_queries)
+    q_starts = cu_seqlens_q[:-1].index_select(0, q_to_seq).to(torch.int32)
+    k_starts = cu_seqlens_k[:-1].index_select(0, q_to_seq).to(torch.int32)
+    cached_lens = (k_lens - q_lens).index_select(0, q_to_seq)
+    local_q = torch.arange(num_queries, dtype=torch.int32, device=q_fp8.device) - q_starts
+    ks = k_starts.contiguous()
+    ke = (ks + cached_lens + local_q + 1).contiguous()
+
+    chunk_rows = _prefill_mqa_chunk_rows(num_queries, total_k, q_fp8.device, max_rows=query_chunk)
+    use_fused_topk = index_topk == 2048
+    valid_lens = (ke - ks).contiguous()
+    for start in range(0, num_queries, chunk_rows):
+        end = min(start + chunk_rows, num_queries)
+        logits = deep_gemm.fp8_mqa_logits(q_fp8[start:end], kv_fp8, weights[start:end], ks[start:end],
+                                          ke[start:end], clean_logits=not use_fused_topk)
+        if use_fused_topk:
+            topk_transform_ragged(logits, valid_lens[start:end], ks[start:end], ks[start:end],
+                                  indices[start:end], index_topk)
+        else:
+            actual_topk = min(index_topk, total_k)
+            top_values, logical = logits.topk(actual_topk, dim=-1)
+            logical = logical.to(torch.int32).masked_fill_(~torch.isfinite(top_values), -1)
+            if actual_topk < index_topk:
+                logical = torch.nn.functional.pad(logical, (0, index_topk - actual_topk), value=-1)
+            indices[start:end] = logical
+            del top_values, logical
+        del logits
+    return indices

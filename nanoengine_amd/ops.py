@@ -456,3 +456,20 @@ def mqa_logits(q_fp8: torch.Tensor, kv_fp8: torch.Tensor, kv_scale: torch.Tensor
     _lib.call("dsa_mqa_logits", _as_bytes(q_fp8).data_ptr(), _as_bytes(kv2).data_ptr(), sc.data_ptr(),
               weights.data_ptr(), weights.stride(0), ks.data_ptr(), ke.data_ptr(), m, n, INDEXER_HEADS,
               out.data_ptr(), out.stride(0), out.shape[1], int(bool(clean_logits)), _stream(dev))
+
+
+def gather_indexer_cache(cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                         page_size: int, total_k: int, key_out: torch.Tensor, scale_out: torch.Tensor) -> None:
+    """Paged indexer pages -> ragged keys [total_k, 128] and scale bytes [total_k, 4]
+    (see dsa_gather_indexer_cache)."""
+    _require(cu_seqlens_k.dtype in (torch.int32, torch.int64), "cu_seqlens_k must be int32 or int64", ValueError)
+    _require(block_table.dtype == torch.int32, "block_table must be int32", ValueError)
+    _require(key_out.shape == (total_k, INDEXER_HEAD_DIM) and key_out.dtype == torch.uint8
+             and key_out.is_contiguous(), "key_out must be contiguous uint8 [total_k, 128]", ValueError)
+    _require(scale_out.shape == (total_k, 4) and scale_out.dtype == torch.uint8 and scale_out.is_contiguous(),
+             "scale_out must be contiguous uint8 [total_k, 4]", ValueError)
+    dev = _check_cuda(cache, block_table, cu_seqlens_k, key_out, scale_out)
+    _lib.call("dsa_gather_indexer_cache", cache.data_ptr(), cache.stride(0), int(page_size), INDEXER_HEAD_DIM,
+              block_table.data_ptr(), block_table.stride(0), cu_seqlens_k.data_ptr(),
+              int(cu_seqlens_k.dtype == torch.int64), block_table.shape[0], int(total_k), key_out.data_ptr(),
+              scale_out.data_ptr(), _stream(dev))

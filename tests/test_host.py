@@ -64,3 +64,29 @@ def test_golden_fixture_reproduces_from_the_oracle():
         k = min(int(L), 2048)
         ref = torch.topk(torch.from_numpy(g["logits"][b, :L]), k).indices.numpy()
         assert set(ref.tolist()) == set(raw[b, :k].tolist())
+
+
+def test_prefill_mqa_chunk_rows_respects_available_memory(monkeypatch):
+    """Chunk sizing from free memory (lightning.py:381-405; the reference's
+    tests/test_indexer_prefill.py:228-237 cases)."""
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda _device: (1_000_000, 10_000_000))
+    dev = torch.device("cuda")
+    assert indexer._prefill_mqa_chunk_rows(100, 100_000, dev) == 1
+    assert indexer._prefill_mqa_chunk_rows(100, 100_000, dev, max_rows=7) == 1
+    assert indexer._prefill_mqa_chunk_rows(10, 100, dev) == 10
+    assert indexer._prefill_mqa_chunk_rows(10, 100, dev, max_rows=3) == 3
+    with pytest.raises(ValueError):
+        indexer._prefill_mqa_chunk_rows(10, 0, dev)
+    assert indexer._prefill_mqa_chunk_rows(0, 10, dev) == 0
+
+
+def test_gather_indexer_cache_argument_checks():
+    from nanoengine_amd.indexer_cache_gather import gather_indexer_cache
+    cache = torch.zeros(4, 64 * 132, dtype=torch.uint8)
+    bt = torch.zeros(2, 3, dtype=torch.int32)
+    with pytest.raises(ValueError, match="cu_seqlens_k and block_table batch dimensions differ"):
+        gather_indexer_cache(cache, bt, torch.tensor([0, 5]), page_size=64, head_dim=128)
+    with pytest.raises(ValueError, match="Indexer cache page has"):
+        gather_indexer_cache(cache, bt, torch.tensor([0, 5, 9]), page_size=32, head_dim=128)
+    with pytest.raises(ValueError, match="contiguous 2D uint8"):
+        gather_indexer_cache(cache.float(), bt, torch.tensor([0, 5, 9]), page_size=64, head_dim=128)
