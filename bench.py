@@ -52,9 +52,10 @@ def parse_args():
     p.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample")
     p.add_argument("--copy-calib", action="store_true")
     p.add_argument("--unfused", action="store_true", help="indexer logits + top-k as two operators")
-    p.add_argument("--config", type=int, choices=[2, 3], default=2,
+    p.add_argument("--config", type=int, choices=[2, 3, 4], default=2,
                    help="2: decode B=128 x 64K (the headline); 3: MTP verify, B=64, next_n=2, "
-                        "lognormal lengths (median 16K, clipped to 2K-128K)")
+                        "lognormal lengths (median 16K, clipped to 2K-128K); 4: chunked prefill, "
+                        "8192 queries over a 120K cached prefix (128K keys)")
     p.add_argument("--only", choices=["fused", "indexer", "topk", "mla"], default=None,
                    help="profiling aid: launch only this stage in the timed loop (no JSON line)")
     return p.parse_args()
@@ -154,6 +155,83 @@ def prologue_stages(T, dev, seed, reps=50):
     return out
 
 
+def bench_prefill(args):
+    """one 8192-token chunk over a 122880-token cached prefix
+    (131072 keys in all). Stages, each timed with HIP events on the launch
+    stream over `steps` repetitions: the paged-to-ragged key gather, the ragged
+    fp8 MQA logits [8192 x 131072] (causal windows), and the ragged top-2048."""
+    import torch
+
+    from nanoengine_amd import _lib, ops, synth
+    from nanoengine_amd.indexer import gather_indexer_cache
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    QN, KN, K = 8192, 131072, args.topk
+    inp = synth.make_indexer_inputs([KN], next_n=1, seed=args.seed, device=dev)
+    dgen = torch.Generator(device=dev).manual_seed(args.seed + 3)
+    q = torch.randn(QN, 64, 128, generator=dgen, device=dev).to(torch.bfloat16)
+    q_codes, q_scale = synth.ue8m0_quant_rows(q)
+    w = (torch.randn(QN, 64, generator=dgen, device=dev) * 64 ** -0.5 * 128 ** -0.5 * q_scale).float().contiguous()
+    q8 = q_codes.view(torch.float8_e4m3fn)
+    cu_k = torch.tensor([0, KN], dtype=torch.int32, device=dev)
+    ks = torch.zeros(QN, dtype=torch.int32, device=dev)
+    ke = (KN - QN + 1 + torch.arange(QN, dtype=torch.int32, device=dev)).contiguous()
+    lens = (ke - ks).contiguous()
+    logits = torch.empty(QN, KN, dtype=torch.float32, device=dev)
+    idx = torch.empty(QN, K, dtype=torch.int32, device=dev)
+    keys, scales = gather_indexer_cache(inp.cache, inp.block_tables, cu_k, page_size=64, head_dim=128, total_k=KN)
+    ws = torch.empty(ops.topk_workspace_bytes(QN), dtype=torch.uint8, device=dev)
+    kvs = scales.view(torch.float32).reshape(-1)
+    stages = [
+        ("gather_indexer_cache", lambda: ops.gather_indexer_cache(inp.cache, inp.block_tables, cu_k, 64, KN, keys,
+                                                                  scales)),
+        ("mqa_logits", lambda: ops.mqa_logits(q8, keys.view(torch.float8_e4m3fn), kvs, w, ks, ke, logits, False)),
+        ("topk_transform_ragged", lambda: ops.topk_transform_ragged(logits, lens, ks, ks, idx, K, workspace=ws)),
+    ]
+    for _ in range(max(1, args.warmup)):
+        for _, fn in stages:
+            fn()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for _, fn in stages:
+            fn()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    out = {}
+    for name, fn in stages:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = {"us": round(e0.elapsed_time(e1) * 1e3 / steps, 1)}
+    pairs = int(lens.sum().item())
+    flops = 2.0 * 64 * 128 * pairs
+    out["mqa_logits"].update({"flops": flops, "pairs": pairs,
+                              "TFLOPs": round(flops / (out["mqa_logits"]["us"] * 1e-6) / 1e12, 1),
+                              "fp8_mfma_frac": round(flops / (out["mqa_logits"]["us"] * 1e-6) / 1e12
+                                                     / FP8_PEAK_TFLOPS, 4),
+                              "logits_bytes": QN * KN * 4})
+    out["topk_transform_ragged"]["GBps"] = round(QN * KN * 4 / (out["topk_transform_ragged"]["us"] * 1e-6) / 1e9, 1)
+    mq = out["mqa_logits"]
+    print(json.dumps({
+        "metric": METRIC, "value": round(QN / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8", "data": "synthetic",
+        "config": {"workload": "BASELINE config 4: chunked-prefill indexer (gather + ragged fp8 MQA logits + "
+                               "ragged top-2048), one layer", "queries": QN, "keys": KN, "cached_prefix": KN - QN,
+                   "index_topk": K, "indexer_heads": 64, "indexer_head_dim": 128, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": mq["TFLOPs"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": mq["fp8_mfma_frac"], "traffic": None, "kernel": "mqa_logits_kernel",
+                     "flops_per_launch": flops, "avg_launch_us": mq["us"]},
+        "stages": out, "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -162,6 +240,9 @@ def main():
         sys.exit(2)
     if args.copy_calib:
         copy_calib()
+        return
+    if args.config == 4:
+        bench_prefill(args)
         return
 
     import torch

@@ -8,16 +8,20 @@
 //
 // This is a GEMM of the (token, head) rows of q [M*64, 128] against the keys
 // [N, 128] with a ReLU-weighted head reduction in the epilogue, so it runs on
-// v_mfma_scale_f32_16x16x128_f8f6f4 (unit scales; K = 128 is one instruction).
-// A workgroup (8 waves) owns 16 query tokens and one chunk of keys; each wave
-// keeps the A operand of its 2 tokens (2 x 64 heads x 128 B) resident in
-// registers for the whole chunk. Keys stream through LDS in 64-key stages
-// (8 KB, three buffers): every wave issues one 1 KB global->LDS copy per
-// stage, already in the lane order of the MFMA B operand, so the operand is
-// two conflict-free ds_read_b128 per 16 keys. Per 16 keys and token: 4 MFMAs
-// (64 heads), ReLU + weight on the 16 accumulators a lane holds, then a
-// 2-shuffle butterfly over the 4 key groups of a stage leaves lane l with key
-// l of the stage: one coalesced 256-byte store per token and stage.
+// v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales), the fp8 shape that issues at
+// the full fp8 rate on gfx950 (the 16x16x128 shape reaches ~78% of it). A
+// workgroup (16 waves, four per SIMD) owns 16 query tokens and one chunk of
+// keys; each wave keeps the A operands of its token (2 head tiles of 32 x 2
+// k-steps of 64 dims) resident in registers for the whole chunk. Four waves
+// per SIMD let the ReLU-weighted epilogue of one wave issue while another's
+// MFMAs run. Keys stream through LDS in 64-key stages (8 KB, three buffers):
+// waves 0-7 each issue one 1 KB global->LDS copy per stage, already in the
+// lane order of the MFMA B operand (32 keys x 64 dims per operand, lane half
+// h holding bytes 32h .. 32h+31 of the 64-dim step), so an operand is two
+// conflict-free ds_read_b128. Per 32 keys and token: 4 MFMAs (2 head tiles x
+// 2 k-steps), ReLU + weight on the 16 heads a lane holds per head tile, then
+// one shuffle pairs the two lane halves: lane l ends with key l of the stage,
+// one coalesced 256-byte store per token and stage.
 //
 // Grid: token blocks x key chunks, with the chunk count a multiple of 8 and
 // chunk c placed on XCD c % 8 (workgroups are dealt to the 8 XCDs round
@@ -30,10 +34,11 @@
 namespace dsa {
 namespace {
 
-constexpr int kPfThreads = 512;
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kPfThreads = 1024;
 constexpr int kPfWaves = kPfThreads / 64;
-constexpr int kPfTokensPerWave = 2;
-constexpr int kPfTokens = kPfWaves * kPfTokensPerWave;  // 16 per workgroup
+constexpr int kPfTokens = kPfWaves;  // one token per wave, 16 per workgroup
 constexpr int kPfStageKeys = 64;
 constexpr int kPfStageBytes = kPfStageKeys * 128;       // 8 KB of keys
 constexpr int kPfBufs = 3;
@@ -63,26 +68,38 @@ __device__ __forceinline__ v8i load32B(const uint8_t* p) {
   return r;
 }
 
+// Lane l's 32-byte operand from two 1 KB chunks: bytes 0-15 at lo + 16l, 16-31 at hi + 16l.
+__device__ __forceinline__ v8i load32B_lds(const uint8_t* lo, const uint8_t* hi, int lane) {
+  const v4i a = *reinterpret_cast<const v4i*>(lo + 16 * lane);
+  const v4i b = *reinterpret_cast<const v4i*>(hi + 16 * lane);
+  v8i r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
 __device__ __forceinline__ float relu(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, 3.402823466e38f); }
 
-// Issue this wave's share of stage `kb` (keys kb .. kb+63) into LDS buffer `buf`:
-// wave w copies 16 B per lane of key group w/2, half w%2 (lane l: key
-// kb + 16(w/2) + l%16, bytes 32(l/16) + 16(w%2) .. +16) to key[buf] +
-// 2048(w/2) + 1024(w%2) + 16 l; lanes 8w .. 8w+7 copy the scales of keys
-// kb + 8w .. +8. Keys past n_keys read key n_keys - 1 (their logits are never stored).
+// Issue this wave's share of stage `kb` (keys kb .. kb+63) into LDS buffer
+// `buf`: wave w < 8 copies chunk w = (key tile kt = w/4, k-step ks = (w/2)%2,
+// half p = w%2): lane l takes key kb + 32kt + l%32, bytes 64ks + 32(l/32) +
+// 16p .. +16, to key[buf] + 1024w + 16l. Lanes 8w .. 8w+7 copy the scales of
+// keys kb + 8w .. +8. Keys past n_keys read key n_keys - 1 (their logits are
+// never stored).
 __device__ __forceinline__ void issue_stage(PfLds* lds, int buf, int64_t kb, int64_t n_keys, const uint8_t* kv,
                                             const float* kv_scale, int wave, int lane) {
-  const int g = wave >> 1, hf = wave & 1;
-  int64_t key = kb + g * 16 + (lane & 15);
+  if (wave >= 8) return;  // eight waves cover the 8 KB stage
+  const int kt = wave >> 2, ks = (wave >> 1) & 1, hp = wave & 1;
+  int64_t key = kb + kt * 32 + (lane & 31);
   key = key < n_keys ? key : n_keys - 1;
-  dma16(kv + key * 128 + (lane >> 4) * 32 + hf * 16, lds_addr(&lds->key[buf][g * 2048 + hf * 1024]));
+  dma16(kv + key * 128 + ks * 64 + (lane >> 5) * 32 + hp * 16, lds_addr(&lds->key[buf][wave * 1024]));
   int64_t sk = kb + lane;
   sk = sk < n_keys ? sk : n_keys - 1;
   if ((lane >> 3) == wave) dma4(kv_scale + sk, lds_addr(&lds->scale[buf][0]));
 }
 
 template <bool kPaged>
-__global__ void __launch_bounds__(kPfThreads, 1)
+__global__ void __launch_bounds__(kPfThreads)
 mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv, const float* __restrict__ kv_scale,
                   const float* __restrict__ weights, int64_t w_stride, const int32_t* __restrict__ ks,
                   const int32_t* __restrict__ ke, int M, int64_t n_keys, int token_blocks, int64_t chunk_keys,
@@ -115,25 +132,24 @@ mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
   lo &= ~(int64_t)(kPfStageKeys - 1);
   const int nstages = (int)((hi - lo + kPfStageKeys - 1) / kPfStageKeys);
 
-  // this wave's two tokens: A operands (head ht*16 + lane%16, bytes 32(lane/16) .. +32) and weights
-  int row[kPfTokensPerWave], rks[kPfTokensPerWave], rke[kPfTokensPerWave];
-  v8i qa[kPfTokensPerWave][4];
-  float w[kPfTokensPerWave][4][4];
-#pragma unroll
-  for (int j = 0; j < kPfTokensPerWave; ++j) {
-    const int rr = r0 + wave * kPfTokensPerWave + j;
-    row[j] = rr;
-    const bool ok = rr < M;
-    const int rc = ok ? rr : M - 1;
-    rks[j] = ok ? ks[rc] : 0;
-    rke[j] = ok ? ke[rc] : 0;
+  // this wave's token: A operands (head tile ht, k-step ks: head 32ht + lane%32,
+  // bytes 64ks + 32(lane/32) .. +32) and the weights of the 16 heads a lane's
+  // accumulator rows hold per head tile (32ht + 8(r/4) + 4(lane/32) + r%4)
+  const int row = r0 + wave;
+  const bool row_ok = row < M;
+  const int rc = row_ok ? row : M - 1;
+  const int rks = row_ok ? ks[rc] : 0, rke = row_ok ? ke[rc] : 0;
+  v8i qa[2][2];
+  float w[2][16];
+  {
     const uint8_t* qb = q + (int64_t)rc * kPfHeads * 128;
     const float* wb = weights + (int64_t)rc * w_stride;
 #pragma unroll
-    for (int ht = 0; ht < 4; ++ht) {
-      qa[j][ht] = load32B(qb + (ht * 16 + (lane & 15)) * 128 + (lane >> 4) * 32);
+    for (int ht = 0; ht < 2; ++ht) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[j][ht][e] = wb[ht * 16 + (lane >> 4) * 4 + e];
+      for (int kst = 0; kst < 2; ++kst) qa[ht][kst] = load32B(qb + (ht * 32 + (lane & 31)) * 128 + kst * 64 + (lane >> 5) * 32);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) w[ht][r] = wb[ht * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
     }
   }
   issue_stage(&lds, 0, lo, n_keys, kv, kv_scale, wave, lane);
@@ -149,45 +165,33 @@ mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
     const int buf = s % kPfBufs;
     const int64_t kb = lo + (int64_t)s * kPfStageKeys;
     const uint8_t* kbuf = lds.key[buf];
-    float part[kPfTokensPerWave][4];
+    float part[2];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const v4i b0 = *reinterpret_cast<const v4i*>(kbuf + g * 2048 + 16 * lane);
-      const v4i b1 = *reinterpret_cast<const v4i*>(kbuf + g * 2048 + 1024 + 16 * lane);
-      v8i kb8;
-      kb8[0] = b0[0]; kb8[1] = b0[1]; kb8[2] = b0[2]; kb8[3] = b0[3];
-      kb8[4] = b1[0]; kb8[5] = b1[1]; kb8[6] = b1[2]; kb8[7] = b1[3];
+    for (int kt = 0; kt < 2; ++kt) {
+      const v8i kb0 = load32B_lds(kbuf + (kt * 4 + 0) * 1024, kbuf + (kt * 4 + 1) * 1024, lane);
+      const v8i kb1 = load32B_lds(kbuf + (kt * 4 + 2) * 1024, kbuf + (kt * 4 + 3) * 1024, lane);
+      const v16f z = {};
+      v16f c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[0][0], kb0, z, 0, 0, 0, 127, 0, 127);
+      v16f c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[1][0], kb0, z, 0, 0, 0, 127, 0, 127);
+      c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[0][1], kb1, c0, 0, 0, 0, 127, 0, 127);
+      c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[1][1], kb1, c1, 0, 0, 0, 127, 0, 127);
+      // c_ht[r]: head 32ht + 8(r/4) + 4(lane/32) + r%4, key kb + 32kt + lane%32
+      float a0 = 0.f, a1 = 0.f;  // two chains: no fma waits on the previous one
 #pragma unroll
-      for (int j = 0; j < kPfTokensPerWave; ++j) {
-        v4f c[4];
-#pragma unroll
-        for (int ht = 0; ht < 4; ++ht)
-          c[ht] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j][ht], kb8, (v4f){0.f, 0.f, 0.f, 0.f},
-                                                                  0, 0, 0, 127, 0, 127);
-        // c[ht][e]: head ht*16 + (lane/16)*4 + e, key kb + 16g + lane%16
-        float acc = 0.f;
-#pragma unroll
-        for (int ht = 0; ht < 4; ++ht)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc = fmaf(w[j][ht][e], relu(c[ht][e]), acc);
-        part[j][g] = acc;
+      for (int r = 0; r < 16; ++r) {
+        a0 = fmaf(w[0][r], relu(c0[r]), a0);
+        a1 = fmaf(w[1][r], relu(c1[r]), a1);
       }
+      part[kt] = a0 + a1;
     }
+    // the two lane halves hold the two halves of the heads: lane l < 32 keeps
+    // key tile 0 (key l), lane l >= 32 key tile 1 (key 32 + l%32 = l)
+    const bool hi32 = lane & 32;
+    const float v = (hi32 ? part[1] : part[0]) + __shfl_xor(hi32 ? part[0] : part[1], 32, 64);
     const float sc = lds.scale[buf][lane];
     const int64_t key = kb + lane;
-#pragma unroll
-    for (int j = 0; j < kPfTokensPerWave; ++j) {
-      // butterfly over the four 16-lane groups: lane group q keeps key group q
-      const bool hi32 = lane & 32;
-      const float s0 = hi32 ? part[j][0] : part[j][2];
-      const float s1 = hi32 ? part[j][1] : part[j][3];
-      const float k0 = (hi32 ? part[j][2] : part[j][0]) + __shfl_xor(s0, 32, 64);
-      const float k1 = (hi32 ? part[j][3] : part[j][1]) + __shfl_xor(s1, 32, 64);
-      const bool hi16 = lane & 16;
-      const float v = (hi16 ? k1 : k0) + __shfl_xor(hi16 ? k0 : k1, 16, 64);
-      if (key >= rks[j] && key < rke[j] && key < hi)
-        __builtin_nontemporal_store(v * sc, logits + (int64_t)row[j] * logits_stride + key);
-    }
+    if (key >= rks && key < rke && key < hi)
+      __builtin_nontemporal_store(v * sc, logits + (int64_t)row * logits_stride + key);
     if (s + 2 < nstages) issue_stage(&lds, (s + 2) % kPfBufs, kb + 2 * kPfStageKeys, n_keys, kv, kv_scale, wave, lane);
   }
 }
