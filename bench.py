@@ -183,11 +183,21 @@ def bench_prefill(args):
     keys, scales = gather_indexer_cache(inp.cache, inp.block_tables, cu_k, page_size=64, head_dim=128, total_k=KN)
     ws = torch.empty(ops.topk_workspace_bytes(QN), dtype=torch.uint8, device=dev)
     kvs = scales.view(torch.float32).reshape(-1)
+    # sparse MLA prefill over the chunk's ragged bf16 keys (cached + fresh), 128 heads
+    H = args.heads
+    kv_bf16 = torch.randn(KN, 576, generator=dgen, device=dev).to(torch.bfloat16)
+    q_mla = torch.randn(QN, H, 576, generator=dgen, device=dev).to(torch.bfloat16)
+    mla_out = torch.empty(QN, H, 512, dtype=torch.bfloat16, device=dev)
+    mla_max = torch.empty(QN, H, dtype=torch.float32, device=dev)
+    mla_lse = torch.empty(QN, H, dtype=torch.float32, device=dev)
+    scale = 192 ** -0.5
     stages = [
         ("gather_indexer_cache", lambda: ops.gather_indexer_cache(inp.cache, inp.block_tables, cu_k, 64, KN, keys,
                                                                   scales)),
         ("mqa_logits", lambda: ops.mqa_logits(q8, keys.view(torch.float8_e4m3fn), kvs, w, ks, ke, logits, False)),
         ("topk_transform_ragged", lambda: ops.topk_transform_ragged(logits, lens, ks, ks, idx, K, workspace=ws)),
+        ("sparse_mla_prefill", lambda: ops.sparse_mla_prefill(q_mla, kv_bf16, idx, scale, out=mla_out,
+                                                              max_logits=mla_max, lse=mla_lse)),
     ]
     for _ in range(max(1, args.warmup)):
         for _, fn in stages:
@@ -216,15 +226,22 @@ def bench_prefill(args):
                               "fp8_mfma_frac": round(flops / (out["mqa_logits"]["us"] * 1e-6) / 1e12
                                                      / FP8_PEAK_TFLOPS, 4),
                               "logits_bytes": QN * KN * 4})
+    mla_pairs = int((idx >= 0).sum().item())
+    mla_flops = 2.0 * H * (576 + 512) * mla_pairs
+    mu = out["sparse_mla_prefill"]["us"]
+    out["sparse_mla_prefill"].update({"flops": mla_flops, "TFLOPs": round(mla_flops / (mu * 1e-6) / 1e12, 1),
+                                      "bf16_mfma_frac": round(mla_flops / (mu * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                      "heads": H})
     out["topk_transform_ragged"]["GBps"] = round(QN * KN * 4 / (out["topk_transform_ragged"]["us"] * 1e-6) / 1e9, 1)
     mq = out["mqa_logits"]
     print(json.dumps({
         "metric": METRIC, "value": round(QN / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "fp8", "data": "synthetic",
-        "config": {"workload": "BASELINE config 4: chunked-prefill indexer (gather + ragged fp8 MQA logits + "
-                               "ragged top-2048), one layer", "queries": QN, "keys": KN, "cached_prefix": KN - QN,
-                   "index_topk": K, "indexer_heads": 64, "indexer_head_dim": 128, "parallelism": "single GPU"},
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8+bf16", "data": "synthetic",
+        "config": {"workload": "BASELINE config 4: chunked prefill (gather + ragged fp8 MQA logits + ragged "
+                               "top-2048 + sparse MLA prefill over bf16 rows), one layer", "queries": QN,
+                   "keys": KN, "cached_prefix": KN - QN, "index_topk": K, "indexer_heads": 64,
+                   "indexer_head_dim": 128, "mla_heads": H, "mla_dims": "576/512", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": mq["TFLOPs"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": mq["fp8_mfma_frac"], "traffic": None, "kernel": "mqa_logits_kernel",
                      "flops_per_launch": flops, "avg_launch_us": mq["us"]},

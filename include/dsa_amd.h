@@ -307,6 +307,28 @@ DSA_API int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, i
                                      int64_t total_k, uint8_t* key_out, uint8_t* scale_out,
                                      void* stream);
 
+
+/* Sparse MLA prefill over ragged bf16 KV rows.
+ *   q          [num_tokens, num_heads, 576] bf16 (row stride q_token_stride, head
+ *              stride q_head_stride elements, last dim contiguous)
+ *   kv         [s_kv, 576] bf16, row stride kv_row_stride elements (>= 576)
+ *   indices    [num_tokens, topk] int32 into kv (row stride idx_stride); entries
+ *              < 0 or >= s_kv are skipped
+ *   out        [num_tokens, num_heads, 512] bf16, contiguous
+ *   max_logits [num_tokens, num_heads] f32 (may be NULL): max_i s_i
+ *   lse        [num_tokens, num_heads] f32 natural-log LSE (may be NULL)
+ * s_i = sm_scale * q . kv[idx_i]; o = softmax(s) @ kv[idx, :512]. A token with no
+ * valid index yields o = 0 and lse = max_logits = -inf.
+ * num_heads % 16 == 0; topk % 32 == 0.
+ * Replaces flash_mla.flash_mla_sparse_fwd(q, kv, indices, sm_scale, d_v=512)
+ * (third-party FlashMLA, called at dlengine/runtime/models/deepseek_v2/
+ *  deepseek_v2.py:1644-1650). */
+DSA_API int dsa_sparse_mla_prefill(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                   const void* kv, int64_t kv_row_stride, int64_t s_kv,
+                                   const int32_t* indices, int64_t idx_stride, int num_tokens,
+                                   int num_heads, int topk, float sm_scale, void* out,
+                                   float* max_logits, float* lse, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -15,7 +15,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libdsa_amd.so"
 SOURCES = ["capi.hip", "topk.hip", "indexer.hip", "sparse_mla.hip", "cache_store.hip",
-           "indexer_prologue.hip", "prefill_logits.hip"]
+           "indexer_prologue.hip", "prefill_logits.hip", "sparse_mla_prefill.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -40,6 +40,7 @@ PER_FILE_FLAGS = {
     "indexer.hip": VGPR_FORM,
     "cache_store.hip": VGPR_FORM,
     "sparse_mla.hip": [],
+    "sparse_mla_prefill.hip": [],
     "indexer_prologue.hip": [],
     "prefill_logits.hip": VGPR_FORM,
 }

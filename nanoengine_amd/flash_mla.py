@@ -1,9 +1,11 @@
-"""The FlashMLA entry points the sparse fp8 decode path calls, on MI355X.
+"""The FlashMLA entry points the DSA path calls, on MI355X.
 
 ``flash_mla_with_kvcache(..., is_fp8_kvcache=True, indices=...)`` with the
 argument order used at dlengine/runtime/layers/backends/mla/flash_mla.py:86-97,
-and ``get_mla_metadata()`` (:80-81). Only the sparse fp8 decode is provided:
-the dense paged decode is not on the DSA path and raises.
+``get_mla_metadata()`` (:80-81), and the sparse prefill
+``flash_mla_sparse_fwd(q, kv, indices, sm_scale, d_v)`` as called at
+dlengine/runtime/models/deepseek_v2/deepseek_v2.py:1644-1650. The dense paged
+decode is not on the DSA path and raises.
 """
 from __future__ import annotations
 
@@ -66,3 +68,24 @@ def flash_mla_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, block_table, 
         splits = int(num_splits)
     o, lse = ops.sparse_mla_decode(q3, k_cache, idx, softmax_scale, num_splits=splits, workspace=ws)
     return o.view(B, n, H, ops.MLA_D_V), lse.view(B, n, H).permute(0, 2, 1)
+
+
+def flash_mla_sparse_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_scale: float,
+                         d_v: int = 512):
+    """Sparse MLA prefill. q [s_q, h_q, 576] bf16; kv [s_kv, h_kv=1, 576] bf16
+    (the chunk's cached + fresh keys, ragged order); indices [s_q, h_kv=1, topk]
+    int32 logical indices into kv (-1 or >= s_kv = skip). Returns
+    (out [s_q, h_q, d_v] bf16, max_logits [s_q, h_q] f32, lse [s_q, h_q] f32,
+    natural log)."""
+    if d_v != ops.MLA_D_V:
+        raise ValueError(f"d_v must be {ops.MLA_D_V}, got {d_v}")
+    if kv.dim() != 3 or kv.shape[1] != 1:
+        raise ValueError(f"kv must be [s_kv, 1, 576] (one KV head), got {tuple(kv.shape)}")
+    if indices.dim() != 3 or indices.shape[1] != 1 or indices.shape[0] != q.shape[0]:
+        raise ValueError(f"indices must be [s_q, 1, topk], got {tuple(indices.shape)}")
+    idx = indices[:, 0, :]
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    if idx.stride(-1) != 1:
+        idx = idx.contiguous()
+    return ops.sparse_mla_prefill(q, kv[:, 0, :], idx, sm_scale)

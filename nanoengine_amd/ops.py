@@ -473,3 +473,36 @@ def gather_indexer_cache(cache: torch.Tensor, block_table: torch.Tensor, cu_seql
               block_table.data_ptr(), block_table.stride(0), cu_seqlens_k.data_ptr(),
               int(cu_seqlens_k.dtype == torch.int64), block_table.shape[0], int(total_k), key_out.data_ptr(),
               scale_out.data_ptr(), _stream(dev))
+
+
+def sparse_mla_prefill(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_scale: float,
+                       out: torch.Tensor | None = None, max_logits: torch.Tensor | None = None,
+                       lse: torch.Tensor | None = None):
+    """Sparse MLA prefill (see dsa_sparse_mla_prefill): q [T, H, 576] bf16, kv
+    [s_kv, 576] bf16 (row stride free), indices [T, topk] int32 into kv.
+    Returns (out [T, H, 512] bf16, max_logits [T, H] f32, lse [T, H] f32)."""
+    _require(q.dim() == 3 and q.shape[2] == MLA_D_QK and q.dtype == torch.bfloat16 and q.stride(2) == 1,
+             f"q must be bf16 [T, H, 576] with a contiguous last dim, got {tuple(q.shape)} {q.dtype}", ValueError)
+    kv2 = kv.reshape(kv.shape[0], -1) if kv.dim() == 3 else kv
+    _require(kv2.dim() == 2 and kv2.shape[1] == MLA_D_QK and kv2.dtype == torch.bfloat16 and kv2.stride(1) == 1,
+             f"kv must be bf16 [s_kv, 576] (or [s_kv, 1, 576]), got {tuple(kv.shape)} {kv.dtype}", ValueError)
+    T, H, _ = q.shape
+    _require(indices.dim() == 2 and indices.shape[0] == T and indices.dtype == torch.int32
+             and indices.stride(1) == 1, "indices must be int32 [T, topk]", ValueError)
+    topk = indices.shape[1]
+    dev = _check_cuda(q, kv2, indices)
+    if out is None:
+        out = torch.empty(T, H, MLA_D_V, dtype=torch.bfloat16, device=dev)
+    if max_logits is None:
+        max_logits = torch.empty(T, H, dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty(T, H, dtype=torch.float32, device=dev)
+    _require(out.shape == (T, H, MLA_D_V) and out.dtype == torch.bfloat16 and out.is_contiguous(),
+             "out must be contiguous bf16 [T, H, 512]", ValueError)
+    for t_, nm in ((max_logits, "max_logits"), (lse, "lse")):
+        _require(t_.shape == (T, H) and t_.dtype == torch.float32 and t_.is_contiguous(),
+                 f"{nm} must be contiguous f32 [T, H]", ValueError)
+    _lib.call("dsa_sparse_mla_prefill", q.data_ptr(), q.stride(0), q.stride(1), kv2.data_ptr(), kv2.stride(0),
+              kv2.shape[0], indices.data_ptr(), indices.stride(0), T, H, topk, float(sm_scale), out.data_ptr(),
+              max_logits.data_ptr(), lse.data_ptr(), _stream(dev))
+    return out, max_logits, lse

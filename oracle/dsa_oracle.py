@@ -28,7 +28,7 @@ __all__ = [
     "topk_indices_to_physical", "sparse_mla_decode", "indexer_decode_topk",
     "rope_cos_sin_cache", "interleaved_to_half", "rope_neox", "hadamard128", "f32_tree_sum128",
     "indexer_q_prologue", "indexer_k_transform", "mqa_logits", "gather_indexer_cache",
-    "prefill_ks_ke",
+    "prefill_ks_ke", "sparse_mla_prefill",
 ]
 
 FP8_MAX = 448.0
@@ -403,6 +403,41 @@ def sparse_mla_decode(q: np.ndarray, kv_rows: np.ndarray, indices: np.ndarray,
         o[t] = ((p / den) @ kv[:, :d_v]).astype(np.float32)
         lse[t] = (m[:, 0] + np.log(den[:, 0])).astype(np.float32)
     return o, lse
+
+
+def sparse_mla_prefill(q: np.ndarray, kv: np.ndarray, indices: np.ndarray, sm_scale: float,
+                       d_v: int = D_NOPE):
+    """Sparse MLA prefill over ragged bf16 rows (the contract of
+    ``flash_mla_sparse_fwd(q, kv, indices, sm_scale, d_v)`` as called at
+    deepseek_v2.py:1644-1650; FlashMLA is third-party and not vendored).
+
+    q float [T,H,576] and kv float [s_kv,576] (bf16 values); indices int [T,K]
+    into kv, entries < 0 or >= s_kv skipped. Per (t,h): ``s_i = scale * q .
+    kv[idx_i]``, ``o = softmax(s) @ kv[idx, :512]``, ``max_logits = max_i s_i``,
+    ``lse = log sum_i exp(s_i)`` (natural log, as the decode path). A query with
+    no valid index gives o = 0, max_logits = lse = -inf. Float64 math.
+    Returns (o float32 [T,H,d_v], max_logits float32 [T,H], lse float32 [T,H]).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    kv = np.asarray(kv, dtype=np.float64)
+    T, H, D = q.shape
+    o = np.zeros((T, H, d_v), dtype=np.float32)
+    mx = np.full((T, H), -np.inf, dtype=np.float32)
+    lse = np.full((T, H), -np.inf, dtype=np.float32)
+    for t in range(T):
+        idx = np.asarray(indices[t]).astype(np.int64)
+        idx = idx[(idx >= 0) & (idx < kv.shape[0])]
+        if idx.size == 0:
+            continue
+        rows = kv[idx]
+        s = (q[t] @ rows[:, :D].T) * sm_scale
+        m = s.max(axis=1, keepdims=True)
+        p = np.exp(s - m)
+        den = p.sum(axis=1, keepdims=True)
+        o[t] = ((p / den) @ rows[:, :d_v]).astype(np.float32)
+        mx[t] = m[:, 0].astype(np.float32)
+        lse[t] = (m[:, 0] + np.log(den[:, 0])).astype(np.float32)
+    return o, mx, lse
 
 
 # --------------------------------------------------------------------------- indexer prologue

@@ -259,3 +259,36 @@ def test_sparse_mla_invalid_rows_and_merge_rule():
     # no valid index: o = 0, lse = -inf
     o0, l0 = O.sparse_mla_decode(q, rows, np.full((1, 64), -1, np.int32), 0.1)
     assert np.all(o0 == 0) and np.all(np.isneginf(l0))
+
+
+def test_sparse_mla_prefill_matches_torch_and_decode_oracle():
+    """The bf16-row prefill oracle against (a) torch softmax / logsumexp / max on
+    the gathered rows, (b) the fp8 decode oracle on the same rows dequantised
+    (fp8 times a power-of-two scale is exact in bf16), (c) the split-and-merge
+    rule, and the skip rules (negative and out-of-range indices)."""
+    rng = np.random.default_rng(12)
+    kv = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((300, 576)).astype(np.float32)))
+    rows8 = O.quantize_mla_rows(kv)
+    kv_deq = O.dequant_mla_rows(rows8)
+    q = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((3, 8, 576)).astype(np.float32)))
+    idx = np.stack([rng.permutation(300)[:128] for _ in range(3)]).astype(np.int32)
+    idx[1, ::3] = -1
+    idx[2, ::5] = 300 + 7          # past s_kv: skipped
+    scale = 192 ** -0.5
+    o, mx, lse = O.sparse_mla_prefill(q, kv_deq, idx, scale)
+    for t in range(3):
+        sel = torch.from_numpy(kv_deq[idx[t][(idx[t] >= 0) & (idx[t] < 300)]]).double()
+        s = torch.from_numpy(q[t]).double() @ sel.T * scale
+        np.testing.assert_allclose(o[t], (torch.softmax(s, -1) @ sel[:, :512]).numpy(), atol=1e-6, rtol=1e-5)
+        np.testing.assert_allclose(lse[t], torch.logsumexp(s, -1).numpy(), atol=1e-5, rtol=0)
+        np.testing.assert_allclose(mx[t], s.max(-1).values.numpy(), atol=1e-5, rtol=0)
+    idx_dec = np.where(idx >= 300, -1, idx)
+    od, ld = O.sparse_mla_decode(q, rows8, idx_dec, scale)
+    np.testing.assert_allclose(o, od, atol=1e-6)
+    np.testing.assert_allclose(lse, ld, atol=1e-6)
+    o1, _, l1 = O.sparse_mla_prefill(q, kv_deq, idx[:, :40], scale)
+    o2, _, l2 = O.sparse_mla_prefill(q, kv_deq, idx[:, 40:], scale)
+    m = np.logaddexp(l1, l2)
+    np.testing.assert_allclose(o1 * np.exp(l1 - m)[..., None] + o2 * np.exp(l2 - m)[..., None], o, atol=1e-5)
+    o0, m0, l0 = O.sparse_mla_prefill(q, kv_deq, np.full((3, 32), -1, np.int32), scale)
+    assert np.all(o0 == 0) and np.all(np.isneginf(l0)) and np.all(np.isneginf(m0))
