@@ -17,8 +17,9 @@
 //            global_load_lds_dwordx4 - consecutive lanes take consecutive
 //            16-byte pieces of the packed rows - into one of three buffers,
 //            two blocks ahead of use. The row indices arrive the same way,
-//            four blocks ahead, in a five-entry ring. Invalid indices read a
-//            zero row.
+//            four blocks ahead, in a five-entry ring; one wave turns a block's
+//            indices into a 64-entry row-address table in LDS, so a load costs
+//            a table read and an add. Invalid indices read a zero row.
 //   QK     : wave (kh = q/2, d = q%2) forms the partial S^T[32 keys x 32
 //            heads] of keys 32kh..32kh+31 over nope dims [256d, 256d+256)
 //            and rope dims [32d, 32d+32). The nope part runs on
@@ -73,7 +74,8 @@ constexpr int kPOff = kMxOff + 2 * 32 * 4 * 4;        // P: [2 hp][4 quarters][6
 constexpr int kEOff = kPOff + 2 * 4 * 64 * 16;        // exponent offsets: [4 tiles][4 k-steps][2 halves][8 u16]
 constexpr int kRingOff = kEOff + 4 * 4 * 2 * 16;      // row indices, one 64-entry block per slot
 constexpr int kRingSlots = 5;
-constexpr size_t kMlaSmemBytes = kRingOff + kRingSlots * 256;
+constexpr int kAddrOff = kRingOff + kRingSlots * 256;  // row addresses of the next block to gather, 64 x u64
+constexpr size_t kMlaSmemBytes = kAddrOff + kMlaKeys * 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
@@ -200,16 +202,33 @@ __device__ __forceinline__ v16f mfma_fp8_chunk(int c, v8i a, v8i b, v16f acc, in
   }
 }
 
-// The gather of one block: prep_rows() reads the row indices from ring slot
-// j % 5 and forms each lane's row address; issue_all() sends this wave's loads.
-struct RowDma {
-  uint64_t rowp;  // this lane's row (lane = row of the block)
-  uint32_t lbuf;
-  int ln;         // lane id, opaque to the compiler (see prep_rows)
-  bool on;
-};
+// The gather of one block. One wave writes the 64 row addresses of the block
+// to a table in LDS (lane = row); every wave then sends its share of the 41
+// wave-wide loads, lane l of load i taking 16-byte piece c = 64(first + i) + l
+// of the packed block: row c / 41, byte 16 (c % 41) of it. Those (row, byte)
+// pairs are loop invariants, computed once per lane (DmaLanes).
+constexpr int kTabWave = 6;  // the wave that builds the row-address table
 
-// Wave w sends loads [first(w), first(w) + count(w)) of the block's 41: six for
+__device__ __forceinline__ uint64_t row_address(const MlaParams& P, int32_t slot) {
+  if (slot < 0) return reinterpret_cast<uint64_t>(g_mla_zero_row);
+  int64_t blk, in_blk;
+  if (P.kv_block_shift >= 0) {
+    blk = slot >> P.kv_block_shift;
+    in_blk = slot & ((1 << P.kv_block_shift) - 1);
+  } else {
+    blk = slot / P.kv_block_size;
+    in_blk = slot % P.kv_block_size;
+  }
+  return reinterpret_cast<uint64_t>(P.kv + blk * P.kv_blk_stride + in_blk * kMlaRowBytes);
+}
+
+// Table of block j's row addresses from ring slot j % 5 (lane = row).
+__device__ __forceinline__ void build_addr_table(const MlaParams& P, uint8_t* smem, int j, int lane) {
+  const int32_t slot = reinterpret_cast<const int32_t*>(smem + kRingOff + (j % kRingSlots) * 256)[lane];
+  *reinterpret_cast<uint64_t*>(smem + kAddrOff + 8 * lane) = row_address(P, slot);
+}
+
+// Wave w sends loads [first(w), first(w) + count(w)) of the block: six for
 // wave 0, five for the others, in runs that share one M0 (LDS base) value.
 __device__ __forceinline__ int dma_count(int wave) {
   return kDmaPerBlock / kMlaWaves + (wave < kDmaPerBlock % kMlaWaves ? 1 : 0);
@@ -220,74 +239,48 @@ __device__ __forceinline__ int dma_first(int wave) {
 static_assert(kDmaPerBlock / kMlaWaves == 5 && kDmaPerBlock % kMlaWaves == 1,
               "wait_vm() counts 6 / 5 loads per wave");
 
-__device__ __forceinline__ uint64_t row_dma_addr(const RowDma& g, int i) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int c = 64 * (dma_first(wave) + i) + g.ln;  // 16-byte piece of the packed block
-  const int r = min(c / kMlaRowPieces, kMlaKeys - 1);
-  const int piece = c - r * kMlaRowPieces;
-  return __shfl(g.rowp, r, 64) + 16 * piece;
+// Load i of this lane: table byte offset 8 * row in bits 0-15, byte offset
+// within the row in bits 16-31.
+struct DmaLanes {
+  uint32_t pk[6];
+};
+
+__device__ __forceinline__ DmaLanes dma_lanes(int wave, int lane) {
+  DmaLanes d;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int c = 64 * (dma_first(wave) + i) + lane;
+    const int r = min(c / kMlaRowPieces, kMlaKeys - 1);
+    d.pk[i] = (uint32_t)(8 * r) | ((uint32_t)(16 * (c - r * kMlaRowPieces)) << 16);
+  }
+  return d;
 }
 
-__device__ __forceinline__ void prep_rows(RowDma& g, const MlaParams& P, const uint8_t* smem, int j,
-                                          const uint8_t* buf, int lane, bool on) {
-  g.on = on;
-  if (!on) return;
-  const int32_t slot = reinterpret_cast<const int32_t*>(smem + kRingOff + (j % kRingSlots) * 256)[lane];
-  if (slot >= 0) {
-    int64_t blk, in_blk;
-    if (P.kv_block_shift >= 0) {
-      blk = slot >> P.kv_block_shift;
-      in_blk = slot & ((1 << P.kv_block_shift) - 1);
-    } else {
-      blk = slot / P.kv_block_size;
-      in_blk = slot % P.kv_block_size;
-    }
-    g.rowp = reinterpret_cast<uint64_t>(P.kv + blk * P.kv_blk_stride + in_blk * kMlaRowBytes);
-  } else {
-    g.rowp = reinterpret_cast<uint64_t>(g_mla_zero_row);
-  }
-  g.lbuf = __builtin_amdgcn_readfirstlane(lds_addr(buf));
-  // an opaque lane id keeps the per-load lane offsets from being hoisted out
-  // of the block loop, where they would pin registers for the whole kernel
-  g.ln = lane;
-  asm volatile("" : "+v"(g.ln));
+__device__ __forceinline__ uint64_t dma_addr(const uint8_t* smem, uint32_t pk) {
+  return *reinterpret_cast<const uint64_t*>(smem + kAddrOff + (pk & 0xffffu)) + (pk >> 16);
 }
 
-// Send loads i .. i+n-1 (n <= 4) of this wave with one M0 value: the
-// immediate offset moves both the global and the LDS address by 1 KB steps.
-__device__ __forceinline__ void issue_run(const RowDma& g, int i, int n, int wave) {
-  if (!g.on) return;
-  const uint32_t m0 = g.lbuf + 1024 * (dma_first(wave) + i);
-  const uint32_t m = __builtin_amdgcn_readfirstlane(m0);
-  const uint64_t a0 = row_dma_addr(g, i);
-  if (n == 1) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(a0), "{m0}"(m) : "memory");
-    return;
-  }
-  const uint64_t a1 = row_dma_addr(g, i + 1) - 1024;
-  if (n == 2) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024"
-                 ::"v"(a0), "v"(a1), "{m0}"(m) : "memory");
-    return;
-  }
-  const uint64_t a2 = row_dma_addr(g, i + 2) - 2048;
-  const uint64_t a3 = row_dma_addr(g, i + 3) - 3072;
+// Send this wave's loads of a block into `buf` (the table must hold its rows):
+// runs of up to four share one M0 value, the immediate offset moving both the
+// global and the LDS address by 1 KB steps.
+__device__ __forceinline__ void issue_block(const uint8_t* smem, const DmaLanes& d, const uint8_t* buf, int wave) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(buf) + 1024 * dma_first(wave));
+  const uint64_t a0 = dma_addr(smem, d.pk[0]);
+  const uint64_t a1 = dma_addr(smem, d.pk[1]) - 1024;
+  const uint64_t a2 = dma_addr(smem, d.pk[2]) - 2048;
+  const uint64_t a3 = dma_addr(smem, d.pk[3]) - 3072;
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024\n\t"
                "global_load_lds_dwordx4 %2, off offset:2048\n\tglobal_load_lds_dwordx4 %3, off offset:3072"
-               ::"v"(a0), "v"(a1), "v"(a2), "v"(a3), "{m0}"(m) : "memory");
-}
-
-// All of this wave's loads of the block: 4 + 2 (wave 0) or 4 + 1.
-__device__ __forceinline__ void issue_all(const RowDma& g, int wave) {
-  issue_run(g, 0, 4, wave);
-  issue_run(g, 4, dma_count(wave) - 4, wave);
-}
-
-__device__ __forceinline__ void issue_rows(const MlaParams& P, const uint8_t* smem, int j, uint8_t* buf,
-                                           int lane, int wave) {
-  RowDma g;
-  prep_rows(g, P, smem, j, buf, lane, true);
-  issue_all(g, wave);
+               ::"v"(a0), "v"(a1), "v"(a2), "v"(a3), "{m0}"(m0) : "memory");
+  const uint32_t m1 = __builtin_amdgcn_readfirstlane(lds_addr(buf) + 1024 * (dma_first(wave) + 4));
+  const uint64_t b0 = dma_addr(smem, d.pk[4]);
+  if (dma_count(wave) == 6) {
+    const uint64_t b1 = dma_addr(smem, d.pk[5]) - 1024;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024"
+                 ::"v"(b0), "v"(b1), "{m0}"(m1) : "memory");
+  } else {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(b0), "{m0}"(m1) : "memory");
+  }
 }
 
 __device__ __forceinline__ void issue_index(const MlaParams& P, uint8_t* smem, int t, int key_begin, int j,
@@ -405,8 +398,16 @@ sparse_mla_kernel(const MlaParams P) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   barrier();
-  issue_rows(P, smem, 0, smem, lane, wave);
-  if (nblk > 1) issue_rows(P, smem, 1, smem + kBufBytes, lane, wave);
+  const DmaLanes dl = dma_lanes(wave, lane);
+  if (wave == kTabWave) build_addr_table(P, smem, 0, lane);
+  barrier();
+  issue_block(smem, dl, smem, wave);
+  if (nblk > 1) {
+    barrier();  // every wave has read block 0's addresses
+    if (wave == kTabWave) build_addr_table(P, smem, 1, lane);
+    barrier();
+    issue_block(smem, dl, smem + kBufBytes, wave);
+  }
 
   float* xs_mine = reinterpret_cast<float*>(smem + kXsOff) + (wave * 64 + lane) * 8;
   const float* xs_part = reinterpret_cast<const float*>(smem + kXsOff) + ((wave ^ 1) * 64 + lane) * 8;
@@ -424,6 +425,8 @@ sparse_mla_kernel(const MlaParams P) {
     const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kRingOff + (n % kRingSlots) * 256)[lane];
     const uint64_t vmask = __ballot(slot_n >= 0);
     if (wave == kIdxWave && n + 4 < nblk) issue_index(P, smem, t, key_begin, n + 4, lane);
+    // row addresses of block n+2 (its indices landed before this barrier), read after B3
+    if (wave == kTabWave && n + 2 < nblk) build_addr_table(P, smem, n + 2, lane);
 
     // Exponent table of this block: entry (tile, key) = the tile scale's
     // exponent shifted into the bf16 exponent field, at the position the PV
@@ -589,11 +592,7 @@ sparse_mla_kernel(const MlaParams P) {
       }
     }
     // block n+2's rows, into the buffer of block n-1 that every wave left at B0
-    {
-      RowDma g;
-      prep_rows(g, P, smem, n + 2, smem + ((n + 2) % kNumBufs) * kBufBytes, lane, n + 2 < nblk);
-      issue_all(g, wave);
-    }
+    if (n + 2 < nblk) issue_block(smem, dl, smem + ((n + 2) % kNumBufs) * kBufBytes, wave);
   }
 
   // drain: nothing may be left in flight when the workgroup ends
