@@ -71,11 +71,11 @@ constexpr int kNumBufs = 3;
 constexpr int kXsOff = kNumBufs * kBufBytes;          // score partials: [8 waves][64 lanes][8 f32]
 constexpr int kMxOff = kXsOff + kMlaWaves * 64 * 32;  // block maxima / final sums: [2 hp][32 heads][4 quarters] f32
 constexpr int kPOff = kMxOff + 2 * 32 * 4 * 4;        // P: [2 hp][4 quarters][64 lanes][8 bf16]
-constexpr int kEOff = kPOff + 2 * 4 * 64 * 16;        // exponent offsets: [4 tiles][4 k-steps][2 halves][8 u16]
-constexpr int kRingOff = kEOff + 4 * 4 * 2 * 16;      // row indices, one 64-entry block per slot
+constexpr int kEOff = kPOff + 2 * 4 * 64 * 16;        // exponent offsets, two blocks: [2][4 tiles][4 k-steps][2 halves][8 u16]
+constexpr int kRingOff = kEOff + 2 * 4 * 4 * 2 * 16;  // row indices, one 64-entry block per slot
 constexpr int kRingSlots = 5;
-constexpr int kAddrOff = kRingOff + kRingSlots * 256;  // row addresses of the next block to gather, 64 x u64
-constexpr size_t kMlaSmemBytes = kAddrOff + kMlaKeys * 8;
+constexpr int kAddrOff = kRingOff + kRingSlots * 256;  // row addresses of blocks being gathered, [2][64] u64
+constexpr size_t kMlaSmemBytes = kAddrOff + 2 * kMlaKeys * 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
@@ -119,10 +119,11 @@ __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
-// Wait until at most n of this wave's copies are outstanding (n in {0, 5, 6}).
+// Wait until at most n of this wave's copies are outstanding (n in {0, 1, 5, 6}).
 __device__ __forceinline__ void wait_vm(int n) {
   if (n >= 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
   else if (n == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+  else if (n >= 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 __device__ __forceinline__ void barrier() {
@@ -222,10 +223,10 @@ __device__ __forceinline__ uint64_t row_address(const MlaParams& P, int32_t slot
   return reinterpret_cast<uint64_t>(P.kv + blk * P.kv_blk_stride + in_blk * kMlaRowBytes);
 }
 
-// Table of block j's row addresses from ring slot j % 5 (lane = row).
+// Table of block j's row addresses from ring slot j % 5 (lane = row), in table j % 2.
 __device__ __forceinline__ void build_addr_table(const MlaParams& P, uint8_t* smem, int j, int lane) {
   const int32_t slot = reinterpret_cast<const int32_t*>(smem + kRingOff + (j % kRingSlots) * 256)[lane];
-  *reinterpret_cast<uint64_t*>(smem + kAddrOff + 8 * lane) = row_address(P, slot);
+  *reinterpret_cast<uint64_t*>(smem + kAddrOff + (j & 1) * 512 + 8 * lane) = row_address(P, slot);
 }
 
 // Wave w sends loads [first(w), first(w) + count(w)) of the block: six for
@@ -256,26 +257,28 @@ __device__ __forceinline__ DmaLanes dma_lanes(int wave, int lane) {
   return d;
 }
 
-__device__ __forceinline__ uint64_t dma_addr(const uint8_t* smem, uint32_t pk) {
-  return *reinterpret_cast<const uint64_t*>(smem + kAddrOff + (pk & 0xffffu)) + (pk >> 16);
+__device__ __forceinline__ uint64_t dma_addr(const uint8_t* tab, uint32_t pk) {
+  return *reinterpret_cast<const uint64_t*>(tab + (pk & 0xffffu)) + (pk >> 16);
 }
 
 // Send this wave's loads of a block into `buf` (the table must hold its rows):
 // runs of up to four share one M0 value, the immediate offset moving both the
 // global and the LDS address by 1 KB steps.
-__device__ __forceinline__ void issue_block(const uint8_t* smem, const DmaLanes& d, const uint8_t* buf, int wave) {
+__device__ __forceinline__ void issue_block(const uint8_t* smem, int j, const DmaLanes& d, const uint8_t* buf,
+                                            int wave) {
+  const uint8_t* tab = smem + kAddrOff + (j & 1) * 512;
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(buf) + 1024 * dma_first(wave));
-  const uint64_t a0 = dma_addr(smem, d.pk[0]);
-  const uint64_t a1 = dma_addr(smem, d.pk[1]) - 1024;
-  const uint64_t a2 = dma_addr(smem, d.pk[2]) - 2048;
-  const uint64_t a3 = dma_addr(smem, d.pk[3]) - 3072;
+  const uint64_t a0 = dma_addr(tab, d.pk[0]);
+  const uint64_t a1 = dma_addr(tab, d.pk[1]) - 1024;
+  const uint64_t a2 = dma_addr(tab, d.pk[2]) - 2048;
+  const uint64_t a3 = dma_addr(tab, d.pk[3]) - 3072;
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024\n\t"
                "global_load_lds_dwordx4 %2, off offset:2048\n\tglobal_load_lds_dwordx4 %3, off offset:3072"
                ::"v"(a0), "v"(a1), "v"(a2), "v"(a3), "{m0}"(m0) : "memory");
   const uint32_t m1 = __builtin_amdgcn_readfirstlane(lds_addr(buf) + 1024 * (dma_first(wave) + 4));
-  const uint64_t b0 = dma_addr(smem, d.pk[4]);
+  const uint64_t b0 = dma_addr(tab, d.pk[4]);
   if (dma_count(wave) == 6) {
-    const uint64_t b1 = dma_addr(smem, d.pk[5]) - 1024;
+    const uint64_t b1 = dma_addr(tab, d.pk[5]) - 1024;
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off\n\tglobal_load_lds_dwordx4 %1, off offset:1024"
                  ::"v"(b0), "v"(b1), "{m0}"(m1) : "memory");
   } else {
@@ -399,15 +402,16 @@ sparse_mla_kernel(const MlaParams P) {
   }
   barrier();
   const DmaLanes dl = dma_lanes(wave, lane);
-  if (wave == kTabWave) build_addr_table(P, smem, 0, lane);
-  barrier();
-  issue_block(smem, dl, smem, wave);
-  if (nblk > 1) {
-    barrier();  // every wave has read block 0's addresses
-    if (wave == kTabWave) build_addr_table(P, smem, 1, lane);
-    barrier();
-    issue_block(smem, dl, smem + kBufBytes, wave);
+  if (wave == kTabWave) {
+    build_addr_table(P, smem, 0, lane);
+    if (nblk > 1) build_addr_table(P, smem, 1, lane);
   }
+  barrier();
+  issue_block(smem, 0, dl, smem, wave);
+  if (nblk > 1) issue_block(smem, 1, dl, smem + kBufBytes, wave);
+  // rows of block 0 have landed
+  wait_vm(nblk > 1 ? my_dma : 0);
+  barrier();
 
   float* xs_mine = reinterpret_cast<float*>(smem + kXsOff) + (wave * 64 + lane) * 8;
   const float* xs_part = reinterpret_cast<const float*>(smem + kXsOff) + ((wave ^ 1) * 64 + lane) * 8;
@@ -416,17 +420,17 @@ sparse_mla_kernel(const MlaParams P) {
   uint16_t* etab = reinterpret_cast<uint16_t*>(smem + kEOff);
 
   for (int n = 0; n < nblk; ++n) {
-    // B0: rows of block n (and, for the index wave, the indices of block n+2) have landed
-    int allow = n + 1 < nblk ? my_dma : 0;
-    if (wave == kIdxWave && n >= 1 && n + 3 < nblk) allow += 1;
-    wait_vm(allow);
-    barrier();
+    // Block n's rows landed (and are visible) at the last barrier of block n-1.
+    // The buffers, tables and rings a wave touches before its first barrier of
+    // block n are ones no wave still in block n-1 reads: the exponent and address
+    // tables are double-buffered by block parity.
     const uint8_t* buf = smem + (n % kNumBufs) * kBufBytes;
     const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kRingOff + (n % kRingSlots) * 256)[lane];
     const uint64_t vmask = __ballot(slot_n >= 0);
     if (wave == kIdxWave && n + 4 < nblk) issue_index(P, smem, t, key_begin, n + 4, lane);
-    // row addresses of block n+2 (its indices landed before this barrier), read after B3
+    // row addresses of block n+2 (its indices landed before the last barrier), read after B3
     if (wave == kTabWave && n + 2 < nblk) build_addr_table(P, smem, n + 2, lane);
+    uint16_t* et = etab + (n & 1) * 256;
 
     // Exponent table of this block: entry (tile, key) = the tile scale's
     // exponent shifted into the bf16 exponent field, at the position the PV
@@ -437,7 +441,7 @@ sparse_mla_kernel(const MlaParams P) {
       const uint32_t sb = *reinterpret_cast<const uint32_t*>(buf + key * kMlaRowBytes + 512 + 4 * tile);
       const int e = (int)((sb >> 23) & 0xffu) - 127;
       const int pos = ((tile * 4 + (key >> 4)) * 2 + ((key >> 2) & 1)) * 8 + 4 * ((key >> 3) & 1) + (key & 3);
-      etab[pos] = (uint16_t)((uint32_t)(e << 7) & 0xffffu);
+      et[pos] = (uint16_t)((uint32_t)(e << 7) & 0xffffu);
     }
 
     // ---- partial S^T[32 keys x 32 heads] over this wave's dims:
@@ -543,6 +547,9 @@ sparse_mla_kernel(const MlaParams P) {
                       cvt_pk_bf16(pv[6], pv[7])};
       *reinterpret_cast<v4i*>(pbuf + (o4 * 64 + lane) * 16) = pw;
     }
+    // rows of block n+1 have landed: issued at the end of block n-1 (or in the
+    // prologue); only the index wave's load of block n+4 went out after them
+    if (n + 1 < nblk) wait_vm(wave == kIdxWave && n + 4 < nblk ? 1 : 0);
     barrier();  // B3
 
     // ---- O[32 heads x 128 dims] += P' . V over the block's 64 keys (four k-steps of 16).
@@ -575,7 +582,7 @@ sparse_mla_kernel(const MlaParams P) {
           for (int nn = 0; nn < 4; ++nn) vr[(ks + 1) & 1][nn] = lds_read_tr8_at(p + 32 * nn);
         }
         const v4i pr = *reinterpret_cast<const v4i*>(pbuf + (ks * 64 + lane) * 16);
-        const v4i ev = *reinterpret_cast<const v4i*>(etab + ((jt * 4 + ks) * 2 + h) * 8);
+        const v4i ev = *reinterpret_cast<const v4i*>(et + ((jt * 4 + ks) * 2 + h) * 8);
         v4i pa;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -591,8 +598,8 @@ sparse_mla_kernel(const MlaParams P) {
           o[nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa), vb16[nn], o[nn], 0, 0, 0);
       }
     }
-    // block n+2's rows, into the buffer of block n-1 that every wave left at B0
-    if (n + 2 < nblk) issue_block(smem, dl, smem + ((n + 2) % kNumBufs) * kBufBytes, wave);
+    // block n+2's rows, into the buffer of block n-1, which every wave left before B3
+    if (n + 2 < nblk) issue_block(smem, n + 2, dl, smem + ((n + 2) % kNumBufs) * kBufBytes, wave);
   }
 
   // drain: nothing may be left in flight when the workgroup ends
