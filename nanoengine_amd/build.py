@@ -31,8 +31,8 @@ HIPCC_FLAGS = [
 ]
 # MFMA results in VGPRs where the accumulators feed VALU work (ReLU, top-k
 # keys) every step and AGPR-resident results would cost a copy each time. The
-# sparse-MLA kernel keeps its output accumulators in AGPRs instead: with 1 wave
-# per SIMD it needs more than the 256 architectural VGPRs.
+# sparse-MLA kernels and the prologue use the compiler's default register
+# assignment.
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 PER_FILE_FLAGS = {
     "capi.hip": VGPR_FORM,
