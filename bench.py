@@ -399,7 +399,7 @@ def main():
     achieved = gbs(idx_bytes, filt_us)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": r4(achieved / HBM_PEAK_GBS), "traffic": pmc_traffic() if step.fused else None,
-                "kernel": "indexer_logits_kernel<1, kIdxFilter>" if step.fused else "indexer_logits_kernel<1, kIdxStore>",
+                "kernel": "indexer_filter_kernel<1> (persistent filter pass)" if step.fused else "indexer_logits_kernel<1, kIdxStore>",
                 "bytes_per_launch": idx_bytes, "avg_launch_us": round(filt_us, 2)}
 
     stages["outside_step"] = prologue_stages(B * n, dev, args.seed)

@@ -120,37 +120,61 @@ __device__ __forceinline__ T shfl_xor(T v, int mask) {
 // Block-wide (NT threads): find the bin tb with S(tb+1) < remain <= S(tb),
 // S(b) = sum of hist[b..nbins). Leaves tb, above = S(tb+1), eq = hist[tb] in
 // the shared *tb_out, *above_out, *eq_out for every thread after the call.
+// nbins is a power of two <= 4096; hist is 16-byte aligned. Thread t owns
+// bins [t*per, t*per + per), read once (16-byte reads when per >= 4).
 template <int NT>
 __device__ void find_threshold(const uint32_t* hist, uint32_t* wave_sum, int nbins, uint32_t remain,
                                uint32_t* tb_out, uint32_t* above_out, uint32_t* eq_out) {
   constexpr int kWaves = NT / 64;
+  constexpr int kMaxPer = 4096 / NT;
+  static_assert(kMaxPer % 4 == 0, "4096 bins over at most 1024 threads");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = nbins >= NT ? nbins / NT : 1;
   const int first = tid * per;
+  uint32_t v[kMaxPer];
+#pragma unroll
+  for (int i = 0; i < kMaxPer; ++i) v[i] = 0u;
+  if (per >= 4) {
+#pragma unroll
+    for (int i = 0; i < kMaxPer; i += 4)
+      if (i < per) {
+        const uint4 x = *reinterpret_cast<const uint4*>(hist + first + i);
+        v[i] = x.x; v[i + 1] = x.y; v[i + 2] = x.z; v[i + 3] = x.w;
+      }
+  } else if (first < nbins) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < per) v[i] = hist[first + i];
+  }
   uint32_t local = 0;
-  if (first < nbins)
-    for (int i = 0; i < per; ++i) local += hist[first + i];
+#pragma unroll
+  for (int i = 0; i < kMaxPer; ++i) local += v[i];
   // inclusive suffix sum inside the wave
-  uint32_t v = local;
+  uint32_t sfx = local;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    uint32_t n = __shfl_down(v, off, 64);
-    if (lane + off < 64) v += n;
+    uint32_t n = __shfl_down(sfx, off, 64);
+    if (lane + off < 64) sfx += n;
   }
-  if (lane == 0) wave_sum[wave] = v;
+  if (lane == 0) wave_sum[wave] = sfx;
   __syncthreads();
-  uint32_t higher = v - local;
-  for (int w = wave + 1; w < kWaves; ++w) higher += wave_sum[w];
-  if (first < nbins) {
+  uint32_t higher = sfx - local;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w)
+    if (w > wave) higher += wave_sum[w];
+  if (first < nbins && higher < remain && higher + local >= remain) {
     uint32_t acc = higher;
-    for (int i = per - 1; i >= 0; --i) {
-      uint32_t h = hist[first + i];
-      if (acc < remain && acc + h >= remain) {
-        *tb_out = first + i;
-        *above_out = acc;
-        *eq_out = h;
+#pragma unroll
+    for (int i = kMaxPer - 1; i >= 0; --i) {
+      if (i < per) {
+        const uint32_t h = v[i];
+        if (acc < remain && acc + h >= remain) {
+          *tb_out = first + i;
+          *above_out = acc;
+          *eq_out = h;
+        }
+        acc += h;
       }
-      acc += h;
     }
   }
   __syncthreads();

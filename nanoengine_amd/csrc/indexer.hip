@@ -79,12 +79,20 @@ struct IdxStageNone {
   uint32_t unused;
 };
 
-constexpr int kSamplePagesPerWave = 4;
-constexpr int kSamplePages = kIdxWaves * kSamplePagesPerWave;  // 16 sampled pages per row, one workgroup
+constexpr int kSamplePages = 16;  // sampled pages per row, one workgroup
+// The sample pass is latency-bound (one workgroup per row): its pages are
+// spread one per wave (two per wave for two query tokens, which need twice the
+// query registers).
+template <int NQ>
+constexpr int sample_threads() { return NQ == 1 ? 1024 : 512; }
+template <int NQ, int MODE>
+constexpr int idx_threads() { return MODE == kIdxSample ? sample_threads<NQ>() : kIdxThreads; }
+constexpr int kSampleBinBits = 10;                              // threshold histogram of the sample
+constexpr int kSampleBins = 1 << kSampleBinBits;
 struct IdxSampleLds {
   float logit[2][kSamplePages * kIdxPageTokens];
-  uint32_t hist[4096];
-  uint32_t wave_sum[kIdxWaves];
+  uint32_t hist[kSampleBins];
+  uint32_t wave_sum[2 * 16];
   uint32_t tb, above, eq;
 };
 
@@ -95,6 +103,38 @@ struct IdxStage {  // per-WG LDS staging of kIdxFilter candidates, per query tok
   uint32_t pos[2][kIdxWgTokens];
 };
 
+// Head-weighted ReLU sum of query token j over one page, before the token
+// scale: lane l returns the value of token l of the page.
+template <int NQ>
+__device__ __forceinline__ float page_head_sum(const PageRegs& cur, int j, int lane, const v8i (&qa)[NQ][4],
+                                               const float (&w)[NQ][4][4]) {
+  float part[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    // four independent products per token tile keep the MFMA pipe busy
+    v4f c[4];
+#pragma unroll
+    for (int ht = 0; ht < 4; ++ht)
+      c[ht] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j][ht], cur.k[tt], (v4f){0.f, 0.f, 0.f, 0.f},
+                                                              0, 0, 0, 127, 0, 127);
+    // c[ht][r]: head ht*16 + (lane/16)*4 + r, token tt*16 + lane%16
+    float acc = 0.f;
+#pragma unroll
+    for (int ht = 0; ht < 4; ++ht)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc = fmaf(w[j][ht][r], relu(c[ht][r]), acc);
+    part[tt] = acc;
+  }
+  // Butterfly over the four 16-lane groups: lane group g keeps token tile g.
+  const bool hi32 = lane & 32;
+  const float s0 = hi32 ? part[0] : part[2];
+  const float s1 = hi32 ? part[1] : part[3];
+  const float k0 = (hi32 ? part[2] : part[0]) + shfl_xor(s0, 32);
+  const float k1 = (hi32 ? part[3] : part[1]) + shfl_xor(s1, 32);
+  const bool hi16 = lane & 16;
+  return (hi16 ? k1 : k0) + shfl_xor(hi16 ? k0 : k1, 16);
+}
+
 template <int NQ, int MODE>
 __device__ __forceinline__ void compute_page(const PageRegs& cur, int p, int vp, int lane, const v8i (&qa)[NQ][4],
                                              const float (&w)[NQ][4][4], const int (&L)[NQ],
@@ -103,31 +143,7 @@ __device__ __forceinline__ void compute_page(const PageRegs& cur, int p, int vp,
   IdxStage* stage = static_cast<IdxStage*>(lds);
 #pragma unroll
   for (int j = 0; j < NQ; ++j) {
-    float part[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      // four independent products per token tile keep the MFMA pipe busy
-      v4f c[4];
-#pragma unroll
-      for (int ht = 0; ht < 4; ++ht)
-        c[ht] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j][ht], cur.k[tt], (v4f){0.f, 0.f, 0.f, 0.f},
-                                                                0, 0, 0, 127, 0, 127);
-      // c[ht][r]: head ht*16 + (lane/16)*4 + r, token tt*16 + lane%16
-      float acc = 0.f;
-#pragma unroll
-      for (int ht = 0; ht < 4; ++ht)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc = fmaf(w[j][ht][r], relu(c[ht][r]), acc);
-      part[tt] = acc;
-    }
-    // Butterfly over the four 16-lane groups: lane group g keeps token tile g.
-    const bool hi32 = lane & 32;
-    const float s0 = hi32 ? part[0] : part[2];
-    const float s1 = hi32 ? part[1] : part[3];
-    const float k0 = (hi32 ? part[2] : part[0]) + shfl_xor(s0, 32);
-    const float k1 = (hi32 ? part[3] : part[1]) + shfl_xor(s1, 32);
-    const bool hi16 = lane & 16;
-    const float v = (hi16 ? k1 : k0) + shfl_xor(hi16 ? k0 : k1, 16);
+    const float v = page_head_sum<NQ>(cur, j, lane, qa, w);
     const int t = p * kIdxPageTokens + lane;
     const float logit = t < L[j] ? v * cur.scale : -__builtin_inff();
     if (MODE == kIdxFilter) {
@@ -156,30 +172,41 @@ __device__ __forceinline__ void compute_page(const PageRegs& cur, int p, int vp,
   }
 }
 
-// Two waves per SIMD: three 33-VGPR page buffers, the resident query tiles
-// and head weights take ~180 VGPRs for one query token.
+// Store and filter: 4 waves, two per SIMD: three 33-VGPR page buffers, the
+// resident query tiles and head weights take ~180 VGPRs for one query token.
+// Sample: one workgroup of 16 (8) waves per row.
 template <int NQ, int MODE>
-__global__ void __launch_bounds__(kIdxThreads) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__((idx_threads<NQ, MODE>())) __attribute__((amdgpu_waves_per_eu(2)))
 indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
                       const float* __restrict__ weights, const int32_t* __restrict__ ctx_lens,
                       const int32_t* __restrict__ block_tables, int64_t bt_stride, int64_t max_ctx,
                       const IdxOut o) {
   // LDS: candidate staging (filter) or the sampled logits (sample)
-  __shared__ typename std::conditional<
+  __shared__ __align__(16) typename std::conditional<
       MODE == kIdxFilter, IdxStage,
       typename std::conditional<MODE == kIdxSample, IdxSampleLds, IdxStageNone>::type>::type lds_mem;
   IdxStage* stage = reinterpret_cast<IdxStage*>(&lds_mem);
-  constexpr int PPW = MODE == kIdxSample ? kSamplePagesPerWave : kIdxPagesPerWave;
+  constexpr int NT = idx_threads<NQ, MODE>();
+  constexpr int NW = NT / 64;
+  constexpr int PPW = MODE == kIdxSample ? kSamplePages / NW : kIdxPagesPerWave;
+  static_assert(MODE != kIdxSample || PPW * NW == kSamplePages, "sample geometry");
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int step = MODE == kIdxSample ? o.page_step : 1;
-
   if (MODE == kIdxStore && o.only_failed) {
     bool any = false;
 #pragma unroll
     for (int j = 0; j < NQ; ++j) any |= o.only_failed[b * NQ + j].failed != 0u;
     if (!any) return;
   }
+  const int vp_begin = blockIdx.x * (NW * PPW) + wave;
+  // All of the wave's block-table entries in one load, issued before the
+  // context lengths arrive: every table row holds ceil(max_ctx / 64) entries,
+  // and entries past a row's context are loaded but never used.
+  const int max_pages = (int)((max_ctx + kIdxPageTokens - 1) / kIdxPageTokens);
+  const int spec_page = (vp_begin + NW * lane) * step;
+  const int my_page =
+      (lane < PPW && spec_page < max_pages) ? block_tables[(int64_t)b * bt_stride + spec_page] : 0;
 
   int L[NQ];
   uint32_t tk[NQ];
@@ -194,8 +221,7 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
   // step-th real page)
   const int npages = (int)((min((int64_t)Lmax, max_ctx) + kIdxPageTokens - 1) / kIdxPageTokens);
   const int nvp = (npages + step - 1) / step;
-  const int vp_begin = blockIdx.x * (kIdxWaves * PPW) + wave;
-  if (MODE != kIdxSample && blockIdx.x * (kIdxWaves * PPW) >= nvp) return;
+  if (MODE != kIdxSample && blockIdx.x * (NW * PPW) >= nvp) return;
 
   if (MODE == kIdxFilter) {
     if (threadIdx.x < NQ) stage->count[threadIdx.x] = 0u;
@@ -217,74 +243,126 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
     }
   }
 
-  const int32_t* bt = block_tables + (int64_t)b * bt_stride;
   // Three page buffers rotate so that two pages are in flight while one is
-  // being multiplied; the wave's virtual pages are vp_begin + 4*i.
-  PageRegs buf0, buf1, buf2;
-  auto valid = [&](int i) { return i < PPW && vp_begin + kIdxWaves * i < nvp; };
-  // All of the wave's block-table entries in one load up front, so no page
-  // load waits behind a dependent table read.
-  const int my_page = (lane < PPW && valid(lane)) ? bt[(vp_begin + kIdxWaves * lane) * step] : 0;
+  // being multiplied; the wave's virtual pages are vp_begin + NW*i.
+  [[maybe_unused]] PageRegs buf0, buf1, buf2;
+  auto valid = [&](int i) { return i < PPW && vp_begin + NW * i < nvp; };
   auto page_ptr = [&](int i) {
     return kv + (int64_t)__builtin_amdgcn_readlane(my_page, i) * kIdxPageBytes;
   };
   auto compute = [&](const PageRegs& pr, int i) {
-    const int vp = vp_begin + kIdxWaves * i;
+    const int vp = vp_begin + NW * i;
     compute_page<NQ, MODE>(pr, vp * step, vp, lane, qa, w, L, tk, max_ctx, o, &lds_mem, b);
   };
-  if (valid(0)) load_page(buf0, page_ptr(0), lane);
-  if (valid(1)) load_page(buf1, page_ptr(1), lane);
+  if constexpr (MODE == kIdxSample) {
+    // a latency-bound pass (one workgroup per row): all of a wave's pages in
+    // flight at once
+    PageRegs pb[PPW];
 #pragma unroll
-  for (int i = 0; i < PPW; i += 3) {
-    if (valid(i + 2)) load_page(buf2, page_ptr(i + 2), lane);
-    if (valid(i)) compute(buf0, i);
-    if (valid(i + 3)) load_page(buf0, page_ptr(i + 3), lane);
-    if (valid(i + 1)) compute(buf1, i + 1);
-    if (valid(i + 4)) load_page(buf1, page_ptr(i + 4), lane);
-    if (valid(i + 2)) compute(buf2, i + 2);
+    for (int i = 0; i < PPW; ++i)
+      if (valid(i)) load_page(pb[i], page_ptr(i), lane);
+#pragma unroll
+    for (int i = 0; i < PPW; ++i)
+      if (valid(i)) compute(pb[i], i);
+  } else {
+    if (valid(0)) load_page(buf0, page_ptr(0), lane);
+    if (valid(1)) load_page(buf1, page_ptr(1), lane);
+#pragma unroll
+    for (int i = 0; i < PPW; i += 3) {
+      if (valid(i + 2)) load_page(buf2, page_ptr(i + 2), lane);
+      if (valid(i)) compute(buf0, i);
+      if (valid(i + 3)) load_page(buf0, page_ptr(i + 3), lane);
+      if (valid(i + 1)) compute(buf1, i + 1);
+      if (valid(i + 4)) load_page(buf1, page_ptr(i + 4), lane);
+      if (valid(i + 2)) compute(buf2, i + 2);
+    }
   }
 
   if (MODE == kIdxSample) {
     // The row's score threshold from its sampled logits (one workgroup holds
-    // them all in LDS): the rank-r key of the sample, r = f + 4 sqrt(f) + 8
-    // with f = k * nsample / len (two radix digits, 12 + 10 bits), so that
-    // about k + margin tokens of the whole row are expected at or above it. The
-    // row's candidate list is reset here.
+    // them all in LDS): a key at or below the rank-r key of the sample,
+    // r = f + 4 sqrt(f) + 8 with f = k * nsample / len, so that about k + margin
+    // tokens of the whole row are expected at or above it. Two histogram levels
+    // of 1024 bins over the sample's [min, max] key range (the second inside
+    // the first's bin holding rank r): the threshold is the lower edge of the
+    // final bin holding rank r. Any key at or below the rank-r key is a valid
+    // threshold; resolution only trims the candidate list. The row's
+    // candidate list is reset here.
     IdxSampleLds& sl = *reinterpret_cast<IdxSampleLds*>(&lds_mem);
     const int tid = threadIdx.x;
-    __syncthreads();
     const int span = step * kIdxPageTokens;
+    __syncthreads();  // the sampled logits are in LDS
 #pragma unroll
     for (int j = 0; j < NQ; ++j) {
       RowWs& rw = o.ws[b * NQ + j];
       const float* smp = sl.logit[j];
       const int len = (int)min((int64_t)max(L[j], 0), max_ctx);
       const int nv = (len + span - 1) / span;
+      uint32_t nsample = 0;
+      for (int v = 0; v < nv; ++v) nsample += (uint32_t)max(0, min(len - v * span, kIdxPageTokens));
+      const float fk = (float)nsample / (float)max(len, 1) * (float)o.top_k;
+      const uint32_t r = (uint32_t)(fk + 4.f * sqrtf(fk) + 8.f);
       uint32_t t_key = 0u;  // 0: every token is a candidate
-      if (len > o.top_k) {
-        for (int i = tid; i < 4096; i += kIdxThreads) sl.hist[i] = 0u;
+      if (len > o.top_k && r < nsample) {
+        // this thread's sampled keys (nv * 64 <= 1024 = 4 per thread)
+        constexpr int kPer = kSamplePages * kIdxPageTokens / NT;
+        uint32_t key[kPer];
+        uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          const int e = tid + u * NT;
+          const bool ok = e < nv * kIdxPageTokens && (e >> 6) * span + (e & 63) < len;
+          key[u] = ok ? order_key(smp[e]) : 0u;
+          if (ok) {
+            kmin = min(kmin, key[u]);
+            kmax = max(kmax, key[u]);
+          }
+        }
+        for (int i = tid; i < kSampleBins; i += NT) sl.hist[i] = 0u;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+          kmin = min(kmin, (uint32_t)__shfl_xor(kmin, off, 64));
+          kmax = max(kmax, (uint32_t)__shfl_xor(kmax, off, 64));
+        }
+        if (lane == 0) {
+          sl.wave_sum[wave] = kmin;
+          sl.wave_sum[NW + wave] = kmax;
+        }
         __syncthreads();
-        for (int e = tid; e < nv * kIdxPageTokens; e += kIdxThreads)
-          if ((e >> 6) * span + (e & 63) < len) atomicAdd(&sl.hist[order_key(smp[e]) >> 20], 1u);
-        uint32_t nsample = 0;
-        for (int v = 0; v < nv; ++v) nsample += (uint32_t)max(0, min(len - v * span, kIdxPageTokens));
-        const float fk = (float)nsample / (float)len * (float)o.top_k;
-        const uint32_t r = (uint32_t)(fk + 4.f * sqrtf(fk) + 8.f);
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) {
+          kmin = min(kmin, sl.wave_sum[w2]);
+          kmax = max(kmax, sl.wave_sum[NW + w2]);
+        }
+        const uint32_t range = kmax - kmin;
+        const int shift = max(0, 32 - (int)__clz(range) - kSampleBinBits);
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          const int e = tid + u * NT;
+          if (e < nv * kIdxPageTokens && (e >> 6) * span + (e & 63) < len)
+            atomicAdd(&sl.hist[(key[u] - kmin) >> shift], 1u);
+        }
         __syncthreads();
-        if (r < nsample) {
-          find_threshold<kIdxThreads>(sl.hist, sl.wave_sum, 4096, r, &sl.tb, &sl.above, &sl.eq);
-          const uint32_t tb0 = sl.tb, rem0 = r - sl.above;
+        find_threshold<NT>(sl.hist, sl.wave_sum, kSampleBins, r, &sl.tb, &sl.above, &sl.eq);
+        const uint32_t tb0 = sl.tb;
+        t_key = kmin + (tb0 << shift);
+        if (shift > 0) {
+          // second level inside bin tb0: 10 more bits of the range
+          const uint32_t rem0 = r - sl.above;
+          const int shift2 = max(0, shift - kSampleBinBits);
           __syncthreads();
-          for (int i = tid; i < 1024; i += kIdxThreads) sl.hist[i] = 0u;
+          for (int i = tid; i < kSampleBins; i += NT) sl.hist[i] = 0u;
           __syncthreads();
-          for (int e = tid; e < nv * kIdxPageTokens; e += kIdxThreads)
-            if ((e >> 6) * span + (e & 63) < len) {
-              const uint32_t k = order_key(smp[e]);
-              if ((k >> 20) == tb0) atomicAdd(&sl.hist[(k >> 10) & 1023u], 1u);
-            }
+#pragma unroll
+          for (int u = 0; u < kPer; ++u) {
+            const int e = tid + u * NT;
+            const uint32_t dk = key[u] - kmin;
+            if (e < nv * kIdxPageTokens && (e >> 6) * span + (e & 63) < len && (dk >> shift) == tb0)
+              atomicAdd(&sl.hist[(dk >> shift2) & (kSampleBins - 1)], 1u);
+          }
           __syncthreads();
-          find_threshold<kIdxThreads>(sl.hist, sl.wave_sum, 1024, rem0, &sl.tb, &sl.above, &sl.eq);
-          t_key = (tb0 << 20) | (sl.tb << 10);
+          find_threshold<NT>(sl.hist, sl.wave_sum, kSampleBins, rem0, &sl.tb, &sl.above, &sl.eq);
+          t_key += sl.tb << shift2;
         }
       }
       if (tid == 0) {
@@ -307,7 +385,7 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
       if (threadIdx.x == 0) stage->base[j] = n ? atomicAdd(&rw.count, n) : 0u;
       __syncthreads();
       const uint32_t base = stage->base[j];
-      for (uint32_t e = threadIdx.x; e < n; e += kIdxThreads)
+      for (uint32_t e = threadIdx.x; e < n; e += NT)
         if (base + e < (uint32_t)kListCap) {
           rw.key[base + e] = stage->key[j][e];
           rw.pos[base + e] = stage->pos[j][e];
@@ -316,17 +394,238 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
   }
 }
 
+// ---------------------------------------------------------------- persistent filter pass
+// The filter pass as a persistent kernel: a fixed grid of waves (two
+// workgroups per CU) where each wave streams one contiguous, balanced range
+// of the flattened (batch entry, page) space through its rotating page
+// buffers, with no barriers and no per-workgroup start-up or drain in the
+// loop. Candidates are staged per wave in LDS (wave-uniform counters, no LDS
+// atomics) and flushed to the row's list with one global atomic when the
+// batch entry changes, when the stage could overflow, and at the end.
+constexpr int kFiltStageCap = 384;   // staged candidates per wave and query token
+constexpr int kFiltWindow = 64;      // block-table entries a wave holds (one per lane)
+constexpr int kFiltAdvance = 60;     // pages per window refill (a multiple of the 3- and 4-buffer rotations)
+constexpr int kFiltMaxBatch = 8192;  // batch entries whose page prefix fits in LDS
+struct FiltWaveStage {
+  uint32_t key[2][kFiltStageCap];
+  uint32_t pos[2][kFiltStageCap];
+};
+constexpr size_t filt_smem_bytes(int batch) {
+  return sizeof(FiltWaveStage) * kIdxWaves + ((size_t)batch + 1 + kIdxWaves) * sizeof(int32_t);
+}
+
+template <int NQ>
+__global__ void __launch_bounds__(kIdxThreads) __attribute__((amdgpu_waves_per_eu(2)))
+indexer_filter_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
+                      const float* __restrict__ weights, const int32_t* __restrict__ ctx_lens,
+                      const int32_t* __restrict__ block_tables, int64_t bt_stride, int64_t max_ctx, int batch,
+                      RowWs* __restrict__ ws) {
+  extern __shared__ __align__(16) uint8_t fl_smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  FiltWaveStage& st = reinterpret_cast<FiltWaveStage*>(fl_smem)[wave];
+  int32_t* prefix = reinterpret_cast<int32_t*>(fl_smem + sizeof(FiltWaveStage) * kIdxWaves);  // [batch + 1]
+  int32_t* wsum = prefix + batch + 1;                                                         // [kIdxWaves]
+
+  // 1. pages of each batch entry (the longest of its query tokens, capped at
+  //    max_ctx) -> exclusive prefix in LDS, in tiles of kIdxThreads entries
+  int32_t carry = 0;
+  for (int base = 0; base < batch; base += kIdxThreads) {
+    const int i = base + (int)threadIdx.x;
+    int np = 0;
+    if (i < batch) {
+      int lm = 0;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) lm = max(lm, ctx_lens[i * NQ + j]);
+      np = (int)((min((int64_t)lm, max_ctx) + kIdxPageTokens - 1) / kIdxPageTokens);
+    }
+    int v = np;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int n = __shfl_up(v, off, 64);
+      if (lane >= off) v += n;
+    }
+    if (lane == 63) wsum[wave] = v;
+    __syncthreads();
+    int before = carry, tile = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < kIdxWaves; ++w2) {
+      if (w2 < wave) before += wsum[w2];
+      tile += wsum[w2];
+    }
+    if (i < batch) prefix[i] = before + v - np;
+    carry += tile;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) prefix[batch] = carry;
+  __syncthreads();
+  const int64_t total = carry;
+
+  // 2. this wave's range of the flattened pages
+  const int64_t nwaves = (int64_t)gridDim.x * kIdxWaves;
+  const int64_t gw = (int64_t)blockIdx.x * kIdxWaves + wave;
+  const int64_t p0 = total * gw / nwaves, p1 = total * (gw + 1) / nwaves;
+  const int n = (int)(p1 - p0);
+  if (n <= 0) return;
+
+  // block-table window: lane l holds page p0 + wb + l as (batch entry, table entry)
+  int wb = 0, win_b = 0, win_page = 0;
+  auto refill = [&](int from) {
+    const int64_t p = p0 + from + lane;
+    int bl = 0, page = 0;
+    if (p < p1) {
+      // last batch entry with prefix <= p
+      int lo = 0, hi = batch - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (prefix[mid] <= p) lo = mid; else hi = mid - 1;
+      }
+      bl = lo;
+      page = block_tables[(int64_t)bl * bt_stride + (int)(p - prefix[bl])];
+    }
+    win_b = bl;
+    win_page = page;
+  };
+  refill(0);
+
+  // state of the current batch entry
+  int cur_b = -1;
+  v8i qa[NQ][4];
+  float w[NQ][4][4];
+  int L[NQ];
+  uint32_t tk[NQ];
+  int cnt[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) cnt[j] = 0;
+
+  auto flush = [&](int j) {
+    const int c = cnt[j];
+    if (c == 0) return;
+    RowWs& rw = ws[cur_b * NQ + j];
+    uint32_t base = 0;
+    if (lane == 0) base = atomicAdd(&rw.count, (uint32_t)c);
+    base = __shfl(base, 0, 64);
+    for (int e = lane; e < c; e += 64)
+      if (base + (uint32_t)e < (uint32_t)kListCap) {
+        rw.key[base + e] = st.key[j][e];
+        rw.pos[base + e] = st.pos[j][e];
+      }
+    cnt[j] = 0;
+  };
+  auto enter = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) flush(j);
+    cur_b = b;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const uint8_t* qb = q + ((int64_t)(b * NQ + j) * kIdxHeads) * kIdxHeadDim;
+      const float* wq = weights + (int64_t)(b * NQ + j) * kIdxHeads;
+#pragma unroll
+      for (int ht = 0; ht < 4; ++ht) {
+        qa[j][ht] = load32B(qb + (ht * 16 + (lane & 15)) * kIdxHeadDim + (lane >> 4) * 32);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w[j][ht][r] = wq[ht * 16 + (lane >> 4) * 4 + r];
+      }
+      L[j] = (int)min((int64_t)ctx_lens[b * NQ + j], max_ctx);
+      tk[j] = ws[b * NQ + j].t_key;
+    }
+  };
+
+  auto page_ptr = [&](int k) {
+    return kv + (int64_t)__builtin_amdgcn_readlane(win_page, k - wb) * kIdxPageBytes;
+  };
+  auto compute = [&](const PageRegs& pr, int k) {
+    const int b = __builtin_amdgcn_readlane(win_b, k - wb);
+    if (b != cur_b) enter(b);
+    const int page = (int)(p0 + k - prefix[b]);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      if (cnt[j] > kFiltStageCap - kIdxPageTokens) flush(j);
+      const float v = page_head_sum<NQ>(pr, j, lane, qa, w);
+      const int t = page * kIdxPageTokens + lane;
+      const uint32_t key = order_key(v * pr.scale);
+      const bool pred = t < L[j] && key >= tk[j];
+      const uint64_t m = __ballot(pred);
+      if (pred) {
+        const int slot = cnt[j] + (int)__popcll(m & ((1ull << lane) - 1ull));
+        st.key[j][slot] = key;
+        st.pos[j][slot] = (uint32_t)t;
+      }
+      cnt[j] += (int)__popcll(m);
+    }
+  };
+
+  // NB rotating page buffers, NB - 1 pages in flight while one is multiplied
+  constexpr int NB = NQ == 1 ? 4 : 3;
+  static_assert(kFiltAdvance % NB == 0 && kFiltAdvance + NB - 1 < kFiltWindow, "window refill geometry");
+  PageRegs buf[NB];
+#pragma unroll
+  for (int u = 0; u < NB - 1; ++u)
+    if (u < n) load_page(buf[u], page_ptr(u), lane);
+  for (int k = 0; k < n; k += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (k + u + NB - 1 < n) load_page(buf[(u + NB - 1) % NB], page_ptr(k + u + NB - 1), lane);
+      if (k + u < n) compute(buf[u], k + u);
+    }
+    if (k + NB - wb == kFiltAdvance) {
+      // the NB - 1 pages loaded ahead came from this window's last used lanes
+      wb += kFiltAdvance;
+      refill(wb);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) flush(j);
+}
+
+static int filter_grid() {
+  static int grid = 0;
+  if (grid == 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    grid = 2 * cus;
+  }
+  return grid;
+}
+
+// The persistent filter pass; false when the batch does not fit its LDS prefix.
+static bool launch_filter_persistent(const uint8_t* q, const uint8_t* kv, const float* weights,
+                                     const int32_t* ctx_lens, const int32_t* bt, int64_t bt_stride, int batch,
+                                     int next_n, int64_t max_ctx, RowWs* ws, hipStream_t stream) {
+  if (batch > kFiltMaxBatch) return false;
+  const size_t smem = filt_smem_bytes(batch);
+  static bool attr_set = false;
+  if (!attr_set) {
+    const int max_smem = (int)filt_smem_bytes(kFiltMaxBatch);
+    if (hipFuncSetAttribute((const void*)indexer_filter_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            max_smem) != hipSuccess ||
+        hipFuncSetAttribute((const void*)indexer_filter_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            max_smem) != hipSuccess)
+      return false;
+    attr_set = true;
+  }
+  const dim3 grid((unsigned)filter_grid());
+  if (next_n == 1)
+    hipLaunchKernelGGL(indexer_filter_kernel<1>, grid, dim3(kIdxThreads), smem, stream, q, kv, weights, ctx_lens, bt,
+                       bt_stride, max_ctx, batch, ws);
+  else
+    hipLaunchKernelGGL(indexer_filter_kernel<2>, grid, dim3(kIdxThreads), smem, stream, q, kv, weights, ctx_lens, bt,
+                       bt_stride, max_ctx, batch, ws);
+  return true;
+}
+
 template <int MODE>
 void launch_indexer(const uint8_t* q, const uint8_t* kv, const float* weights, const int32_t* ctx_lens,
                     const int32_t* bt, int64_t bt_stride, int batch, int next_n, int64_t max_ctx, int64_t vpages,
                     const IdxOut& o, hipStream_t stream) {
-  const int64_t per_block = kIdxWaves * (MODE == kIdxSample ? kSamplePagesPerWave : kIdxPagesPerWave);
+  const int64_t per_block = MODE == kIdxSample ? kSamplePages : kIdxWaves * kIdxPagesPerWave;
   const dim3 grid((unsigned)((vpages + per_block - 1) / per_block), (unsigned)batch);
   if (next_n == 1)
-    hipLaunchKernelGGL((indexer_logits_kernel<1, MODE>), grid, dim3(kIdxThreads), 0, stream, q, kv, weights, ctx_lens,
+    hipLaunchKernelGGL((indexer_logits_kernel<1, MODE>), grid, dim3(idx_threads<1, MODE>()), 0, stream, q, kv, weights, ctx_lens,
                        bt, bt_stride, max_ctx, o);
   else
-    hipLaunchKernelGGL((indexer_logits_kernel<2, MODE>), grid, dim3(kIdxThreads), 0, stream, q, kv, weights, ctx_lens,
+    hipLaunchKernelGGL((indexer_logits_kernel<2, MODE>), grid, dim3(idx_threads<2, MODE>()), 0, stream, q, kv, weights, ctx_lens,
                        bt, bt_stride, max_ctx, o);
 }
 
@@ -440,9 +739,12 @@ extern "C" int dsa_indexer_topk(const uint8_t* q_fp8, const uint8_t* kv_cache, c
   if (int rc = check_launch("dsa_indexer_topk(sample)")) return rc;
   mark(1);
   // 3. all pages: candidates at or above the threshold into the row lists
-  IdxOut o_f{nullptr, 0, 1, f.ws, nullptr, top_k};
-  launch_indexer<kIdxFilter>(q_fp8, kv_cache, weights, context_lens, block_tables, block_table_stride, batch, next_n,
-                             max_context_len, max_pages, o_f, st);
+  if (!launch_filter_persistent(q_fp8, kv_cache, weights, context_lens, block_tables, block_table_stride, batch,
+                                next_n, max_context_len, f.ws, st)) {
+    IdxOut o_f{nullptr, 0, 1, f.ws, nullptr, top_k};
+    launch_indexer<kIdxFilter>(q_fp8, kv_cache, weights, context_lens, block_tables, block_table_stride, batch,
+                               next_n, max_context_len, max_pages, o_f, st);
+  }
   if (int rc = check_launch("dsa_indexer_topk(filter)")) return rc;
   mark(2);
   // 4. exact top-k of each usable list (with the page translation)

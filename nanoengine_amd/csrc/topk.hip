@@ -157,7 +157,7 @@ struct RowIn {
 // ---------------------------------------------------------------- 1. threshold
 __global__ void __launch_bounds__(kAuxThreads)
 topk_threshold_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
-  __shared__ uint32_t hist[kHistBins];
+  __shared__ __align__(16) uint32_t hist[kHistBins];
   __shared__ uint32_t wave_sum[kAuxThreads / 64];
   __shared__ uint32_t tb, above, eq;
   const int tid = threadIdx.x, b = blockIdx.x;
@@ -686,21 +686,32 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
   }
   const uint32_t t_key = w.t_key;
 
-  // candidates into LDS as composite (hi = key - t_key, lo = inverted position), and their max
-  uint32_t* hi = s.list_key[0];
-  uint32_t* lo = s.list_pos[0];
+  // Candidates into registers (element e = u * NT + tid), all loads in flight
+  // at once: composite (hi = key - t_key, lo = inverted position), and the
+  // block maximum of hi.
+  constexpr int kPer = kListCap / NT;
+  static_assert(kListCap % NT == 0, "list capacity must be whole rows of the block");
+  uint32_t ch[kPer], cl[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const uint32_t e = (uint32_t)(u * NT + tid);
+    ch[u] = e < cand ? w.key[e] : t_key;
+    cl[u] = e < cand ? w.pos[e] : 0u;
+  }
+  const int nwords = (len + 31) >> 5;
+  for (int i = tid; i < nwords; i += NT) s.bitmap[i] = 0u;
+  for (int i = tid; i < kHistBins; i += NT) s.hist[i] = 0u;
+  if (tid == 0) s.list_count[0] = 0u;
   uint32_t mx = 0;
-  for (uint32_t e = tid; e < cand; e += NT) {
-    const uint32_t rk = w.key[e] - t_key;
-    hi[e] = rk;
-    lo[e] = kIdxMax - w.pos[e];
-    mx = max(mx, rk);
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    ch[u] -= t_key;
+    cl[u] = kIdxMax - cl[u];
+    mx = max(mx, ch[u]);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor(mx, off, 64));
   if (lane == 0) s.wave_sum[wave] = mx;
-  const int nwords = (len + 31) >> 5;
-  for (int i = tid; i < nwords; i += NT) s.bitmap[i] = 0u;
   __syncthreads();
   mx = 0;
   for (int i = 0; i < NT / 64; ++i) mx = max(mx, s.wave_sum[i]);
@@ -714,17 +725,51 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
     const int lo_b = max(top - 12, 0);
     return (uint32_t)((c >> lo_b) & ((1ull << (top - lo_b)) - 1ull));
   };
+  auto mark = [&](uint32_t p) {
+    const uint32_t pos = kIdxMax - p;
+    atomicOr(&s.bitmap[pos >> 5], 1u << (pos & 31));
+  };
 
+  // level 0 straight from the registers
   uint32_t remain = (uint32_t)top_k;
+  bool last;
+  {
+    const int nbins = 1 << (total_bits - max(total_bits - 12, 0));
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+      if ((uint32_t)(u * NT + tid) < cand) atomicAdd(&s.hist[digit(composite(ch[u], cl[u]), 0)], 1u);
+    __syncthreads();
+    find_threshold<NT>(s.hist, s.wave_sum, nbins, remain, &s.tb, &s.above, &s.eq);
+    const uint32_t tb = s.tb, above = s.above, eq = s.eq;
+    remain -= above;
+    last = (eq == remain) || nlev == 1;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      if ((uint32_t)(u * NT + tid) >= cand) continue;
+      const uint32_t d = digit(composite(ch[u], cl[u]), 0);
+      if (d > tb || (last && d == tb)) {
+        mark(cl[u]);
+      } else if (!last && d == tb) {
+        const uint32_t slot = atomicAdd(&s.list_count[0], 1u);
+        s.list_key[0][slot] = ch[u];
+        s.list_pos[0][slot] = cl[u];
+      }
+    }
+    __syncthreads();
+  }
+
+  // further levels over the (short) list of the threshold bin, in LDS
   int cur = 0;
-  uint32_t n = cand;
-  __syncthreads();
-  for (int L = 0; L < nlev; ++L) {
+  for (int L = 1; L < nlev && !last; ++L) {
+    const uint32_t n = s.list_count[cur];
     const int top = total_bits - 12 * L;
     const int lo_b = max(top - 12, 0);
     const int nbins = 1 << (top - lo_b);
+    const int nxt = cur ^ 1;
+    // list_count[cur] is read by every thread above; list_count[nxt] was last
+    // read a level ago
     for (int i = tid; i < nbins; i += NT) s.hist[i] = 0u;
-    if (tid < 2) s.list_count[tid] = 0u;
+    if (tid == 0) s.list_count[nxt] = 0u;
     __syncthreads();
     for (uint32_t e = tid; e < n; e += NT)
       atomicAdd(&s.hist[digit(composite(s.list_key[cur][e], s.list_pos[cur][e]), L)], 1u);
@@ -732,14 +777,12 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
     find_threshold<NT>(s.hist, s.wave_sum, nbins, remain, &s.tb, &s.above, &s.eq);
     const uint32_t tb = s.tb, above = s.above, eq = s.eq;
     remain -= above;
-    const bool last = (eq == remain) || L == nlev - 1;
-    const int nxt = cur ^ 1;
+    last = (eq == remain) || L == nlev - 1;
     for (uint32_t e = tid; e < n; e += NT) {
       const uint32_t h = s.list_key[cur][e], p = s.list_pos[cur][e];
       const uint32_t d = digit(composite(h, p), L);
       if (d > tb || (last && d == tb)) {
-        const uint32_t pos = kIdxMax - p;
-        atomicOr(&s.bitmap[pos >> 5], 1u << (pos & 31));
+        mark(p);
       } else if (!last && d == tb) {
         const uint32_t slot = atomicAdd(&s.list_count[nxt], 1u);
         s.list_key[nxt][slot] = h;
@@ -747,8 +790,6 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
       }
     }
     __syncthreads();
-    if (last) break;
-    n = s.list_count[nxt];
     cur = nxt;
   }
 
