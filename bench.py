@@ -293,11 +293,11 @@ def main():
     torch.cuda.synchronize()
 
     def run(ev=None):
-        # ev: [start, after sample, after filter, after finish, after repair, after MLA]
+        # ev: [start, after sample, after filter, after select, after MLA]
         if step.fused:
             ops.indexer_topk(inp.q_fp8.view(B, n, 64, 128), inp.cache, inp.weights, seq.view(B, n), bt, max_ctx, K,
                              step.physical, step.logical, workspace=step.fused_workspace,
-                             phase_events=ev[0:5] if ev is not None else None)
+                             phase_events=ev[0:4] + [None] if ev is not None else None)
         else:
             if ev is not None:
                 ev[0].record()
@@ -310,11 +310,10 @@ def main():
                                workspace=step.topk_workspace)
             if ev is not None:
                 ev[3].record()
-                ev[4].record()
         ops.sparse_mla_decode(q_mla, kv, step.physical, scale, out=step.out, lse=step.lse,
                               num_splits=step.num_splits, workspace=step.workspace)
         if ev is not None:
-            ev[5].record()
+            ev[4].record()
 
     if args.only:
         run()
@@ -352,14 +351,14 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
 
     # per-phase durations with HIP events on the launch stream (separate pass)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
     for e in evs:
         run(e)
     torch.cuda.synchronize()
-    ph = [[e[i].elapsed_time(e[i + 1]) * 1e3 for e in evs] for i in range(5)]   # us
+    ph = [[e[i].elapsed_time(e[i + 1]) * 1e3 for e in evs] for i in range(4)]   # us
     med = [sorted(x)[len(x) // 2] for x in ph]
     avg = [sum(x) / len(x) for x in ph]
-    idx_total = sum(avg[0:4])
+    idx_total = sum(avg[0:3])
 
     total_tokens = sum(lens)
     # the filter pass reads every key page of every sequence (+ q and head weights)
@@ -379,20 +378,20 @@ def main():
         "indexer_topk": {
             "us": round(idx_total, 2), "fused": step.fused,
             "phases_us": {"sample+threshold": round(avg[0], 2), "filter": round(avg[1], 2),
-                          "finish": round(avg[2], 2), "repair": round(avg[3], 2)},
+                          "select": round(avg[2], 2)},
             "filter_bytes": idx_bytes, "filter_GBps": round(gbs(idx_bytes, avg[1]), 1),
             "filter_hbm_frac": r4(gbs(idx_bytes, avg[1]) / HBM_PEAK_GBS),
             "filter_fp8_mfma_frac": r4(idx_flops / (avg[1] * 1e-6) / 1e12 / FP8_PEAK_TFLOPS)},
-        "sparse_mla_decode": {"us": round(avg[4], 2), "us_median": round(med[4], 2), "bytes": mla_bytes,
-                              "GBps": round(gbs(mla_bytes, avg[4]), 1),
-                              "hbm_frac": r4(gbs(mla_bytes, avg[4]) / HBM_PEAK_GBS),
-                              "bf16_mfma_frac": r4(mla_flops / (avg[4] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS),
+        "sparse_mla_decode": {"us": round(avg[3], 2), "us_median": round(med[3], 2), "bytes": mla_bytes,
+                              "GBps": round(gbs(mla_bytes, avg[3]), 1),
+                              "hbm_frac": r4(gbs(mla_bytes, avg[3]) / HBM_PEAK_GBS),
+                              "bf16_mfma_frac": r4(mla_flops / (avg[3] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS),
                               "num_splits": step.num_splits},
     }
     if not step.fused:
         stages["indexer_topk"] = {"us": round(idx_total, 2), "fused": False,
                                   "phases_us": {"indexer_logits": round(avg[0] + avg[1], 2),
-                                                "topk_transform": round(avg[2] + avg[3], 2)},
+                                                "topk_transform": round(avg[2], 2)},
                                   "indexer_bytes": idx_bytes,
                                   "indexer_GBps": round(gbs(idx_bytes, avg[0] + avg[1]), 1)}
     filt_us = avg[1] if step.fused else avg[0] + avg[1]

@@ -89,14 +89,14 @@ DSA_API size_t dsa_indexer_topk_workspace_bytes(int batch, int next_n, int64_t m
  *   out_logical  [batch*next_n, top_k] int32 token positions (may be NULL)
  * Selection, order (ascending position), ties (lowest positions) and padding are
  * those of dsa_topk_transform over dsa_indexer_logits' logits, exactly.
- * Launch sequence on `stream`: logits of every 32nd page -> per-row score
- * threshold -> all pages, keeping only (key, position) of tokens at or above the
- * threshold in per-row lists -> exact top-k of each list; a row whose list is
- * unusable (fewer than top_k or more than the list capacity) is redone from its
- * full logits by two more launches that return at once for every other row.
+ * Launch sequence on `stream`: logits of 16 sampled pages per row -> per-row
+ * score threshold -> all pages, keeping only (key, position) of tokens at or
+ * above the threshold in per-row lists -> exact top-k of each list; a row whose
+ * list is unusable (fewer than top_k or more than the list capacity) is redone
+ * inside that last launch, by the row's workgroup, from the row's full logits.
  * phase_events: NULL, or five hipEvent_t (entries may be NULL) recorded on
- * `stream` before the first launch and after the sample, filter, finish and
- * repair phases, for timing.
+ * `stream` before the first launch and after the sample, filter and select
+ * phases (the last two entries both after the select), for timing.
  * top_k in {512, 2048}; rows of at most dsa_topk_max_len() positions. The
  * workspace (dsa_indexer_topk_workspace_bytes) should be zero-filled before its
  * first use; a stale one gives the same results, its first call more slowly.

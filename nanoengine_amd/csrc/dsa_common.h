@@ -107,10 +107,24 @@ struct RowWs {
   uint32_t pos[kListCap];
 };
 
-// Launcher of the top-k finish for the fused indexer + top-k entry point (topk.hip).
-int launch_finish_fused(const float* logits, int64_t logits_stride, const int32_t* seq_lens, int64_t max_len,
-                        RowWs* ws, const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
-                        int32_t* out_page, int32_t* out_raw, int top_k, int rows, bool repair, hipStream_t stream);
+// What the list select needs to redo a row whose list is unusable: the
+// indexer inputs of the row (query [rows, 64, 128] fp8, head weights
+// [rows, 64], the paged key cache) and a logits row to write.
+struct RowRepair {
+  const uint8_t* q;
+  const uint8_t* kv;
+  const float* weights;
+  float* logits;
+  int64_t logits_stride;
+};
+
+// Launcher of the list select of the fused indexer + top-k entry point
+// (topk.hip): the exact top-k of each row's candidate list, with the page
+// translation; a row whose list is unusable is redone in place from its
+// full logits.
+int launch_list_select(const RowRepair& rp, const int32_t* seq_lens, int64_t max_len, RowWs* ws,
+                       const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                       int32_t* out_page, int32_t* out_raw, int top_k, int rows, hipStream_t stream);
 
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {

@@ -13,12 +13,12 @@
 // page: the logits row segment and the per-token scales are then one
 // coalesced 256-byte load/store each. Each wave keeps two pages in flight
 // (three rotating register buffers) so that HBM latency overlaps compute.
-//
-// Page layout (bytes): [64 tokens x 128 fp8][64 x f32 scale] = 8448.
+// The page primitives live in indexer_page.h.
 #include <algorithm>
 #include <type_traits>
 
 #include "dsa_common.h"
+#include "indexer_page.h"
 #include "../../include/dsa_amd.h"
 
 namespace dsa {
@@ -26,38 +26,10 @@ namespace dsa {
 constexpr int kIdxThreads = 256;
 constexpr int kIdxWaves = kIdxThreads / 64;
 constexpr int kIdxPagesPerWave = 6;
-constexpr int kIdxPageTokens = 64;
-constexpr int kIdxHeadDim = 128;
-constexpr int kIdxHeads = 64;
-constexpr int kIdxPageBytes = kIdxPageTokens * (kIdxHeadDim + 4);
-
-__device__ __forceinline__ v8i load32B(const uint8_t* p) {
-  const v4i a = *reinterpret_cast<const v4i*>(p);
-  const v4i b = *reinterpret_cast<const v4i*>(p + 16);
-  v8i r;
-  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
-  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
-  return r;
-}
-
-// max(x, 0) in one instruction (v_med3_f32 with bounds 0 and FLT_MAX).
-__device__ __forceinline__ float relu(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, 3.402823466e38f); }
-
-struct PageRegs {
-  v8i k[4];      // token tiles: lane holds token tt*16 + lane%16, bytes (lane/16)*32 .. +32
-  float scale;   // scale of token `lane`
-};
-
-__device__ __forceinline__ void load_page(PageRegs& pr, const uint8_t* page, int lane) {
-  const uint8_t* base = page + (lane & 15) * kIdxHeadDim + (lane >> 4) * 32;
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt) pr.k[tt] = load32B(base + tt * 16 * kIdxHeadDim);
-  pr.scale = reinterpret_cast<const float*>(page + kIdxPageTokens * kIdxHeadDim)[lane];
-}
 
 // What a launch does with the logits of a page.
 enum IdxMode : int {
-  kIdxStore = 0,   // logits[row, t] (and, with `only_failed`, only rows whose list failed)
+  kIdxStore = 0,   // logits[row, t]
   kIdxSample = 1,  // every page_step-th page, one workgroup per row: the logits stay in LDS and
                    // give the row's score threshold ws[row].t_key (lists reset)
   kIdxFilter = 2,  // no logits: (key, t) of every token with key >= ws[row].t_key is appended
@@ -69,7 +41,6 @@ struct IdxOut {
   int64_t logits_stride;
   int page_step;            // kIdxSample: sampled page stride
   RowWs* ws;                // kIdxSample: thresholds out; kIdxFilter: thresholds in, lists out
-  const RowWs* only_failed; // kIdxStore: skip rows whose list was usable (NULL: all rows)
   int top_k;                // kIdxSample
 };
 
@@ -102,38 +73,6 @@ struct IdxStage {  // per-WG LDS staging of kIdxFilter candidates, per query tok
   uint32_t key[2][kIdxWgTokens];
   uint32_t pos[2][kIdxWgTokens];
 };
-
-// Head-weighted ReLU sum of query token j over one page, before the token
-// scale: lane l returns the value of token l of the page.
-template <int NQ>
-__device__ __forceinline__ float page_head_sum(const PageRegs& cur, int j, int lane, const v8i (&qa)[NQ][4],
-                                               const float (&w)[NQ][4][4]) {
-  float part[4];
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    // four independent products per token tile keep the MFMA pipe busy
-    v4f c[4];
-#pragma unroll
-    for (int ht = 0; ht < 4; ++ht)
-      c[ht] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j][ht], cur.k[tt], (v4f){0.f, 0.f, 0.f, 0.f},
-                                                              0, 0, 0, 127, 0, 127);
-    // c[ht][r]: head ht*16 + (lane/16)*4 + r, token tt*16 + lane%16
-    float acc = 0.f;
-#pragma unroll
-    for (int ht = 0; ht < 4; ++ht)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc = fmaf(w[j][ht][r], relu(c[ht][r]), acc);
-    part[tt] = acc;
-  }
-  // Butterfly over the four 16-lane groups: lane group g keeps token tile g.
-  const bool hi32 = lane & 32;
-  const float s0 = hi32 ? part[0] : part[2];
-  const float s1 = hi32 ? part[1] : part[3];
-  const float k0 = (hi32 ? part[2] : part[0]) + shfl_xor(s0, 32);
-  const float k1 = (hi32 ? part[3] : part[1]) + shfl_xor(s1, 32);
-  const bool hi16 = lane & 16;
-  return (hi16 ? k1 : k0) + shfl_xor(hi16 ? k0 : k1, 16);
-}
 
 template <int NQ, int MODE>
 __device__ __forceinline__ void compute_page(const PageRegs& cur, int p, int vp, int lane, const v8i (&qa)[NQ][4],
@@ -193,12 +132,6 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int step = MODE == kIdxSample ? o.page_step : 1;
-  if (MODE == kIdxStore && o.only_failed) {
-    bool any = false;
-#pragma unroll
-    for (int j = 0; j < NQ; ++j) any |= o.only_failed[b * NQ + j].failed != 0u;
-    if (!any) return;
-  }
   const int vp_begin = blockIdx.x * (NW * PPW) + wave;
   // All of the wave's block-table entries in one load, issued before the
   // context lengths arrive: every table row holds ceil(max_ctx / 64) entries,
@@ -652,7 +585,7 @@ extern "C" int dsa_indexer_logits(const uint8_t* q_fp8, const uint8_t* kv_cache,
   if ((reinterpret_cast<uintptr_t>(q_fp8) | reinterpret_cast<uintptr_t>(kv_cache)) & 15)
     return set_error(kInvalidArgument, "indexer: q and kv_cache must be 16-byte aligned");
   const int64_t max_pages = (max_context_len + kIdxPageTokens - 1) / kIdxPageTokens;
-  IdxOut o{logits, logits_stride, 1, nullptr, nullptr, 0};
+  IdxOut o{logits, logits_stride, 1, nullptr, 0};
   launch_indexer<kIdxStore>(q_fp8, kv_cache, weights, context_lens, block_tables, block_table_stride, batch, next_n,
                             max_context_len, max_pages, o, (hipStream_t)stream);
   return check_launch("dsa_indexer_logits");
@@ -668,7 +601,7 @@ static inline int sample_step(int64_t max_pages) {
 
 struct FusedWs {
   RowWs* ws;
-  float* logits;  // full logits, written only for rows redone by the repair launches
+  float* logits;  // full logits, written only for rows the list select redoes
   int64_t logits_stride;
   size_t bytes;
 };
@@ -733,7 +666,7 @@ extern "C" int dsa_indexer_topk(const uint8_t* q_fp8, const uint8_t* kv_cache, c
   const int step = sample_step(max_pages);
   // 1-2. logits of every step-th page (one workgroup per row, kept in LDS) ->
   // the row's score threshold, lists reset
-  IdxOut o_s{nullptr, 0, step, f.ws, nullptr, top_k};
+  IdxOut o_s{nullptr, 0, step, f.ws, top_k};
   launch_indexer<kIdxSample>(q_fp8, kv_cache, weights, context_lens, block_tables, block_table_stride, batch,
                              next_n, max_context_len, (max_pages + step - 1) / step, o_s, st);
   if (int rc = check_launch("dsa_indexer_topk(sample)")) return rc;
@@ -741,25 +674,18 @@ extern "C" int dsa_indexer_topk(const uint8_t* q_fp8, const uint8_t* kv_cache, c
   // 3. all pages: candidates at or above the threshold into the row lists
   if (!launch_filter_persistent(q_fp8, kv_cache, weights, context_lens, block_tables, block_table_stride, batch,
                                 next_n, max_context_len, f.ws, st)) {
-    IdxOut o_f{nullptr, 0, 1, f.ws, nullptr, top_k};
+    IdxOut o_f{nullptr, 0, 1, f.ws, top_k};
     launch_indexer<kIdxFilter>(q_fp8, kv_cache, weights, context_lens, block_tables, block_table_stride, batch,
                                next_n, max_context_len, max_pages, o_f, st);
   }
   if (int rc = check_launch("dsa_indexer_topk(filter)")) return rc;
   mark(2);
-  // 4. exact top-k of each usable list (with the page translation)
-  if (int rc = launch_finish_fused(f.logits, f.logits_stride, context_lens, max_context_len, f.ws, block_tables,
-                                   block_table_stride, next_n, 6u, out_physical, out_logical, top_k, rows, false, st))
-    return rc;
+  // 4. exact top-k of each row's list (with the page translation); a row
+  // whose list is unusable is redone by its workgroup from its full logits
+  const RowRepair rp{q_fp8, kv_cache, weights, f.logits, f.logits_stride};
+  const int rc = launch_list_select(rp, context_lens, max_context_len, f.ws, block_tables, block_table_stride, next_n,
+                                    6u, out_physical, out_logical, top_k, rows, st);
   mark(3);
-  // 5-6. rows whose list was unusable: their full logits, then the full select
-  // (both launches return at once for every other row)
-  IdxOut o_r{f.logits, f.logits_stride, 1, nullptr, f.ws, top_k};
-  launch_indexer<kIdxStore>(q_fp8, kv_cache, weights, context_lens, block_tables, block_table_stride, batch, next_n,
-                            max_context_len, max_pages, o_r, st);
-  if (int rc = check_launch("dsa_indexer_topk(repair)")) return rc;
-  const int rc = launch_finish_fused(f.logits, f.logits_stride, context_lens, max_context_len, f.ws, block_tables,
-                                     block_table_stride, next_n, 6u, out_physical, out_logical, top_k, rows, true, st);
   mark(4);
   return rc;
 }

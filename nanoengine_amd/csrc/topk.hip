@@ -25,6 +25,7 @@
 //      output is deterministic) and written with the page translation.
 // No global sort, no bounded candidate buffer on the exact path.
 #include "dsa_common.h"
+#include "indexer_page.h"
 #include "../../include/dsa_amd.h"
 
 namespace dsa {
@@ -111,12 +112,6 @@ __device__ uint32_t block_exclusive_scan(uint32_t* wave_sum, uint32_t x, uint32_
   return before + v - x;
 }
 
-// topk_finish_kernel modes
-enum FinishMode : int {
-  kFinishNormal = 0,    // list if usable, else the full select over the row
-  kFinishListOnly = 1,  // list if usable, else flag the row (fused indexer: no logits yet)
-  kFinishRepair = 2,    // flagged rows only, full select over their (recomputed) logits
-};
 
 struct RowOut {
   int32_t* page;       // page-translated output (or the untranslated output)
@@ -284,18 +279,15 @@ topk_gather_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
 }
 
 // ---------------------------------------------------------------- 3. finish
-__global__ void __launch_bounds__(kTopkThreads)
-topk_finish_kernel(const RowIn in, RowWs* __restrict__ ws, const int32_t* __restrict__ offsets,
-                   const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
-                   int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k, int mode) {
-  extern __shared__ __align__(16) uint8_t smem_raw[];
-  TopkSmem& s = *reinterpret_cast<TopkSmem*>(smem_raw);
+// The finish of row b by one workgroup of kTopkThreads threads (all of them
+// call it): the list select when the row's list is usable, else the full
+// exact select over the row's scores.
+__device__ void finish_row(TopkSmem& s, const RowIn& in, RowWs* __restrict__ ws, const int32_t* __restrict__ offsets,
+                           const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                           int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k, int b) {
   const int tid = threadIdx.x;
-  const int b = blockIdx.x;
   const int len = in.len(b);
   const float* row = in.row(b);
-  // kFinishRepair: only rows whose list was unusable, from their logits
-  if (mode == kFinishRepair && !ws[b].failed) return;
 
   RowOut out;
   out.page = out_page + (int64_t)b * top_k;
@@ -314,12 +306,7 @@ topk_finish_kernel(const RowIn in, RowWs* __restrict__ ws, const int32_t* __rest
   for (int i = tid; i < kHistBins; i += kTopkThreads) s.hist[i] = 0u;
   if (tid < 2) s.list_count[tid] = 0u;
   const uint32_t cand = ws ? ws[b].count : 0u;
-  const bool listed = ws && mode != kFinishRepair && cand >= (uint32_t)top_k && cand <= (uint32_t)kListCap;
-  if (mode == kFinishListOnly && !listed) {
-    // no logits to fall back on: flag the row for the repair launches
-    if (tid == 0) ws[b].failed = 1u;
-    return;
-  }
+  const bool listed = ws && cand >= (uint32_t)top_k && cand <= (uint32_t)kListCap;
   __syncthreads();
 
   uint32_t thr[kLevels] = {0, 0, 0, 0, 0};
@@ -432,6 +419,15 @@ topk_finish_kernel(const RowIn in, RowWs* __restrict__ ws, const int32_t* __rest
   }
   __syncthreads();
   for (int i = tid; i < top_k; i += kTopkThreads) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
+}
+
+__global__ void __launch_bounds__(kTopkThreads)
+topk_finish_kernel(const RowIn in, RowWs* __restrict__ ws, const int32_t* __restrict__ offsets,
+                   const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                   int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  finish_row(*reinterpret_cast<TopkSmem*>(smem_raw), in, ws, offsets, page_table, pt_stride, pt_div, page_bits,
+             out_page, out_raw, top_k, blockIdx.x);
 }
 
 // ---------------------------------------------------------------- one launch
@@ -655,10 +651,42 @@ topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const i
 // bit positions of the full select, where most candidates share the top
 // digits. A row whose list is unusable (fewer than k or more than the list
 // capacity) is flagged for the repair launches.
+// Full indexer logits of one row by the calling workgroup (kTopkThreads
+// threads): wave w computes pages w, w + 8, ... of the row through three
+// rotating page buffers, logits[t] for t < len.
+__device__ void repair_row_logits(const RowRepair& rp, const int32_t* __restrict__ bt_row, int row, int len) {
+  constexpr int kWaves = kTopkThreads / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v8i qa[1][4];
+  float w[1][4][4];
+  load_query(rp.q + (int64_t)row * kIdxHeads * kIdxHeadDim, rp.weights + (int64_t)row * kIdxHeads, lane, qa[0],
+             w[0]);
+  float* out = rp.logits + (int64_t)row * rp.logits_stride;
+  const int npages = (len + kIdxPageTokens - 1) / kIdxPageTokens;
+  const int n = npages > wave ? (npages - wave + kWaves - 1) / kWaves : 0;  // this wave's pages
+  auto page_ptr = [&](int i) { return rp.kv + (int64_t)bt_row[wave + kWaves * i] * kIdxPageBytes; };
+  auto compute = [&](const PageRegs& pr, int i) {
+    const float v = page_head_sum<1>(pr, 0, lane, qa, w);
+    const int t = (wave + kWaves * i) * kIdxPageTokens + lane;
+    if (t < len) out[t] = v * pr.scale;
+  };
+  PageRegs buf0, buf1, buf2;
+  if (0 < n) load_page(buf0, page_ptr(0), lane);
+  if (1 < n) load_page(buf1, page_ptr(1), lane);
+  for (int i = 0; i < n; i += 3) {
+    if (i + 2 < n) load_page(buf2, page_ptr(i + 2), lane);
+    compute(buf0, i);
+    if (i + 3 < n) load_page(buf0, page_ptr(i + 3), lane);
+    if (i + 1 < n) compute(buf1, i + 1);
+    if (i + 4 < n) load_page(buf1, page_ptr(i + 4), lane);
+    if (i + 2 < n) compute(buf2, i + 2);
+  }
+}
+
 __global__ void __launch_bounds__(kTopkThreads)
 topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* __restrict__ ws,
                  const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
-                 int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k) {
+                 int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k, const RowRepair rp) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   TopkSmem& s = *reinterpret_cast<TopkSmem*>(smem_raw);
   constexpr int NT = kTopkThreads;
@@ -681,7 +709,13 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
   }
   const uint32_t cand = w.count;
   if (cand < (uint32_t)top_k || cand > (uint32_t)kListCap) {
+    // The sample misjudged this row's threshold: its list cannot give the
+    // exact top-k. Redo the row here, from its full logits.
     if (tid == 0) w.failed = 1u;
+    repair_row_logits(rp, page_table + (int64_t)(b / pt_div) * pt_stride, b, len);
+    __syncthreads();  // the row's logits (global) are visible to the whole workgroup
+    const RowIn in{rp.logits, rp.logits_stride, seq_lens, nullptr, max_len};
+    finish_row(s, in, nullptr, nullptr, page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k, b);
     return;
   }
   const uint32_t t_key = w.t_key;
@@ -880,23 +914,17 @@ static int launch_topk(const RowIn& in, int batch, const int32_t* offsets, const
                          top_k, ws);
   }
   hipLaunchKernelGGL(topk_finish_kernel, dim3(batch), dim3(kTopkThreads), kTopkSmemBytes, stream, in, ws,
-                     offsets, page_table, pt_stride, 1, page_bits, out_page, out_raw, top_k, (int)kFinishNormal);
+                     offsets, page_table, pt_stride, 1, page_bits, out_page, out_raw, top_k);
   return check_launch(what);
 }
 
-int launch_finish_fused(const float* logits, int64_t logits_stride, const int32_t* seq_lens, int64_t max_len,
-                        RowWs* ws, const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
-                        int32_t* out_page, int32_t* out_raw, int top_k, int rows, bool repair, hipStream_t stream) {
+int launch_list_select(const RowRepair& rp, const int32_t* seq_lens, int64_t max_len, RowWs* ws,
+                       const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                       int32_t* out_page, int32_t* out_raw, int top_k, int rows, hipStream_t stream) {
   if (int rc = prepare_topk_kernel()) return rc;
-  if (!repair) {
-    hipLaunchKernelGGL(topk_list_kernel, dim3(rows), dim3(kTopkThreads), kTopkSmemBytes, stream, seq_lens, max_len,
-                       ws, page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k);
-    return check_launch("dsa_indexer_topk(select)");
-  }
-  const RowIn in{logits, logits_stride, seq_lens, nullptr, max_len};
-  hipLaunchKernelGGL(topk_finish_kernel, dim3(rows), dim3(kTopkThreads), kTopkSmemBytes, stream, in, ws, nullptr,
-                     page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k, (int)kFinishRepair);
-  return check_launch("dsa_indexer_topk(repair select)");
+  hipLaunchKernelGGL(topk_list_kernel, dim3(rows), dim3(kTopkThreads), kTopkSmemBytes, stream, seq_lens, max_len, ws,
+                     page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k, rp);
+  return check_launch("dsa_indexer_topk(select)");
 }
 
 }  // namespace dsa

@@ -117,8 +117,9 @@ def indexer_topk(q_fp8: torch.Tensor, kv_cache: torch.Tensor, weights: torch.Ten
     """Fused indexer + exact top-k + page translation (see dsa_indexer_topk):
     the same result as topk_transform over indexer_logits, without the logits.
     ``phase_events``: optional five torch.cuda.Event recorded before the first
-    launch and after the sample, filter, finish and repair phases (on the
-    current stream)."""
+    launch and after the sample, filter and select phases (the last two both
+    after the select, which also redoes rows whose list was unusable), on the
+    current stream."""
     _require(q_fp8.dim() == 4, f"q_fp8 must be [B, next_n, H, D], got {tuple(q_fp8.shape)}")
     B, n, H, D = q_fp8.shape
     _require(q_fp8.dtype in (torch.float8_e4m3fn, torch.uint8) and q_fp8.is_contiguous(), "q_fp8 fp8 contiguous")

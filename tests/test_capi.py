@@ -75,7 +75,7 @@ def test_argument_errors_return_status_without_a_device(lib):
 def test_workspace_size_queries(lib):
     assert lib.dsa_topk_workspace_bytes(0) == 0
     assert lib.dsa_topk_workspace_bytes(128) == 128 * (16 + 8 * 6144)
-    # fused indexer + top-k: lists + full logits for the repair launches
+    # fused indexer + top-k: lists + full logits for rows the list select redoes
     assert lib.dsa_indexer_topk_workspace_bytes(0, 1, 65536) == 0
     assert lib.dsa_indexer_topk_workspace_bytes(128, 1, 65536) >= 128 * (16 + 8 * 6144) + 128 * 65536 * 4
     assert lib.dsa_sparse_mla_workspace_bytes(128, 128, 1) == 0

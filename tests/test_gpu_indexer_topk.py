@@ -3,8 +3,8 @@
 The fused call must select exactly what topk_transform selects over the
 logits of indexer_logits on the same inputs (same logits bit for bit, so the
 comparison is exact), for plain decode, MTP rows (next_n = 2), short rows and
-both top-k sizes, and also when the 1/32 page sample misleads the threshold and
-the repair launches have to redo a row from its full logits."""
+both top-k sizes, and also when the page sample misleads the threshold and the
+list select has to redo a row from its full logits."""
 import numpy as np
 import pytest
 import torch
@@ -66,7 +66,7 @@ def test_misleading_sample_takes_the_repair_path(cuda):
     """Row 0: the sampled pages (every 32nd) score 16x higher, so the threshold
     lands above almost every other token and the list is too short. Row 1: the
     sampled pages score 16x lower, so nearly every token passes and the list
-    overflows. Both rows must come out exact through the repair launches."""
+    overflows. Both rows must come out exact through the in-place repair."""
     lens = [65536, 65536, 30000]
     inp, cl, max_ctx = _inputs(lens, 1, seed=5)
     scales = inp.cache[:, 64 * 128:].view(torch.float32)  # [pages, 64] per-token key scales
