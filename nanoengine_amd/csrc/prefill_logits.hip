@@ -14,14 +14,14 @@
 // keys; each wave keeps the A operands of its token (2 head tiles of 32 x 2
 // k-steps of 64 dims) resident in registers for the whole chunk. Four waves
 // per SIMD let the ReLU-weighted epilogue of one wave issue while another's
-// MFMAs run. Keys stream through LDS in 64-key stages (8 KB, three buffers):
-// waves 0-7 each issue one 1 KB global->LDS copy per stage, already in the
+// MFMAs run. Keys stream through LDS in 128-key stages (16 KB, three buffers):
+// each wave issues one 1 KB global->LDS copy per stage, already in the
 // lane order of the MFMA B operand (32 keys x 64 dims per operand, lane half
 // h holding bytes 32h .. 32h+31 of the 64-dim step), so an operand is two
 // conflict-free ds_read_b128. Per 32 keys and token: 4 MFMAs (2 head tiles x
 // 2 k-steps), ReLU + weight on the 16 heads a lane holds per head tile, then
-// one shuffle pairs the two lane halves: lane l ends with key l of the stage,
-// one coalesced 256-byte store per token and stage.
+// one shuffle pairs the two lane halves: lane l ends with key l of each 64-key
+// half of the stage, one coalesced 256-byte store per token and half.
 //
 // Grid: token blocks x key chunks, with the chunk count a multiple of 8 and
 // chunk c placed on XCD c % 8 (workgroups are dealt to the 8 XCDs round
@@ -39,8 +39,9 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kPfThreads = 1024;
 constexpr int kPfWaves = kPfThreads / 64;
 constexpr int kPfTokens = kPfWaves;  // one token per wave, 16 per workgroup
-constexpr int kPfStageKeys = 64;
-constexpr int kPfStageBytes = kPfStageKeys * 128;       // 8 KB of keys
+constexpr int kPfStageKeys = 128;
+constexpr int kPfStageBytes = kPfStageKeys * 128;       // 16 KB of keys
+constexpr int kPfKeyTiles = kPfStageKeys / 32;
 constexpr int kPfBufs = 3;
 constexpr int kPfHeads = 64;
 
@@ -80,22 +81,23 @@ __device__ __forceinline__ v8i load32B_lds(const uint8_t* lo, const uint8_t* hi,
 
 __device__ __forceinline__ float relu(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, 3.402823466e38f); }
 
-// Issue this wave's share of stage `kb` (keys kb .. kb+63) into LDS buffer
-// `buf`: wave w < 8 copies chunk w = (key tile kt = w/4, k-step ks = (w/2)%2,
+// Issue this wave's share of stage `kb` (keys kb .. kb+127) into LDS buffer
+// `buf`: wave w copies chunk w = (key tile kt = w/4, k-step ks = (w/2)%2,
 // half p = w%2): lane l takes key kb + 32kt + l%32, bytes 64ks + 32(l/32) +
-// 16p .. +16, to key[buf] + 1024w + 16l. Lanes 8w .. 8w+7 copy the scales of
-// keys kb + 8w .. +8. Keys past n_keys read key n_keys - 1 (their logits are
-// never stored).
+// 16p .. +16, to key[buf] + 1024w + 16l. In the wave w of each group of
+// eight, lanes 8(w%8) .. +8 copy the scales of keys kb + 64(w/8) + 8(w%8) .. +8.
+// Keys past n_keys read key n_keys - 1 (their logits are never stored).
 __device__ __forceinline__ void issue_stage(PfLds* lds, int buf, int64_t kb, int64_t n_keys, const uint8_t* kv,
                                             const float* kv_scale, int wave, int lane) {
-  if (wave >= 8) return;  // eight waves cover the 8 KB stage
+  static_assert(kPfWaves * 1024 == kPfStageBytes, "one 1 KB chunk per wave");
   const int kt = wave >> 2, ks = (wave >> 1) & 1, hp = wave & 1;
   int64_t key = kb + kt * 32 + (lane & 31);
   key = key < n_keys ? key : n_keys - 1;
   dma16(kv + key * 128 + ks * 64 + (lane >> 5) * 32 + hp * 16, lds_addr(&lds->key[buf][wave * 1024]));
-  int64_t sk = kb + lane;
+  const int half = wave >> 3;
+  int64_t sk = kb + 64 * half + lane;
   sk = sk < n_keys ? sk : n_keys - 1;
-  if ((lane >> 3) == wave) dma4(kv_scale + sk, lds_addr(&lds->scale[buf][0]));
+  if ((lane >> 3) == (wave & 7)) dma4(kv_scale + sk, lds_addr(&lds->scale[buf][64 * half]));
 }
 
 template <bool kPaged>
@@ -165,33 +167,41 @@ mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
     const int buf = s % kPfBufs;
     const int64_t kb = lo + (int64_t)s * kPfStageKeys;
     const uint8_t* kbuf = lds.key[buf];
-    float part[2];
+    // two 64-key halves per stage, each finished (stored) before the next, so
+    // that the registers hold one half's operands and partial sums at a time
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const v8i kb0 = load32B_lds(kbuf + (kt * 4 + 0) * 1024, kbuf + (kt * 4 + 1) * 1024, lane);
-      const v8i kb1 = load32B_lds(kbuf + (kt * 4 + 2) * 1024, kbuf + (kt * 4 + 3) * 1024, lane);
-      const v16f z = {};
-      v16f c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[0][0], kb0, z, 0, 0, 0, 127, 0, 127);
-      v16f c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[1][0], kb0, z, 0, 0, 0, 127, 0, 127);
-      c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[0][1], kb1, c0, 0, 0, 0, 127, 0, 127);
-      c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[1][1], kb1, c1, 0, 0, 0, 127, 0, 127);
-      // c_ht[r]: head 32ht + 8(r/4) + 4(lane/32) + r%4, key kb + 32kt + lane%32
-      float a0 = 0.f, a1 = 0.f;  // two chains: no fma waits on the previous one
+    for (int g = 0; g < kPfKeyTiles / 2; ++g) {
+      __builtin_amdgcn_sched_barrier(0);
+      float part[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        a0 = fmaf(w[0][r], relu(c0[r]), a0);
-        a1 = fmaf(w[1][r], relu(c1[r]), a1);
+      for (int t = 0; t < 2; ++t) {
+        const int kt = 2 * g + t;
+        const v8i kb0 = load32B_lds(kbuf + (kt * 4 + 0) * 1024, kbuf + (kt * 4 + 1) * 1024, lane);
+        const v8i kb1 = load32B_lds(kbuf + (kt * 4 + 2) * 1024, kbuf + (kt * 4 + 3) * 1024, lane);
+        const v16f z = {};
+        v16f c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[0][0], kb0, z, 0, 0, 0, 127, 0, 127);
+        v16f c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[1][0], kb0, z, 0, 0, 0, 127, 0, 127);
+        c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[0][1], kb1, c0, 0, 0, 0, 127, 0, 127);
+        c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[1][1], kb1, c1, 0, 0, 0, 127, 0, 127);
+        // c_ht[r]: head 32ht + 8(r/4) + 4(lane/32) + r%4, key kb + 32kt + lane%32
+        float a0 = 0.f, a1 = 0.f;  // two chains: no fma waits on the previous one
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          a0 = fmaf(w[0][r], relu(c0[r]), a0);
+          a1 = fmaf(w[1][r], relu(c1[r]), a1);
+        }
+        part[t] = a0 + a1;
       }
-      part[kt] = a0 + a1;
+      // the two lane halves hold the two halves of the heads: lane l < 32
+      // keeps the half's first key tile (key l), lane l >= 32 its second
+      // (key 32 + l%32 = l)
+      const bool hi32 = lane & 32;
+      const float v = (hi32 ? part[1] : part[0]) + __shfl_xor(hi32 ? part[0] : part[1], 32, 64);
+      const float sc = lds.scale[buf][64 * g + lane];
+      const int64_t key = kb + 64 * g + lane;
+      if (key >= rks && key < rke && key < hi)
+        __builtin_nontemporal_store(v * sc, logits + (int64_t)row * logits_stride + key);
     }
-    // the two lane halves hold the two halves of the heads: lane l < 32 keeps
-    // key tile 0 (key l), lane l >= 32 key tile 1 (key 32 + l%32 = l)
-    const bool hi32 = lane & 32;
-    const float v = (hi32 ? part[1] : part[0]) + __shfl_xor(hi32 ? part[0] : part[1], 32, 64);
-    const float sc = lds.scale[buf][lane];
-    const int64_t key = kb + lane;
-    if (key >= rks && key < rke && key < hi)
-      __builtin_nontemporal_store(v * sc, logits + (int64_t)row * logits_stride + key);
     if (s + 2 < nstages) issue_stage(&lds, (s + 2) % kPfBufs, kb + 2 * kPfStageKeys, n_keys, kv, kv_scale, wave, lane);
   }
 }
