@@ -733,6 +733,28 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
     cl[u] = e < cand ? w.pos[e] : 0u;
   }
   const int nwords = (len + 31) >> 5;
+  // The row's page table, when it fits in the bitmap words past the row's,
+  // is copied to LDS with the candidates so that the output's translation
+  // reads LDS, not a dependent global load.
+  const int npg = out.pt ? (len + (1 << page_bits) - 1) >> page_bits : 0;
+  const int pt_off = (nwords + 3) & ~3;
+  const bool pt_lds = out.pt && pt_off + npg <= kBitmapWords;
+  int32_t* const ptc = reinterpret_cast<int32_t*>(s.bitmap + pt_off);
+  if (pt_lds) {
+    for (int i0 = 0; i0 < npg; i0 += 4 * NT) {
+      int32_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * NT + tid;
+        v[u] = i < npg ? out.pt[i] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * NT + tid;
+        if (i < npg) ptc[i] = v[u];
+      }
+    }
+  }
   for (int i = tid; i < nwords; i += NT) s.bitmap[i] = 0u;
   for (int i = tid; i < kHistBins; i += NT) s.hist[i] = 0u;
   if (tid == 0) s.list_count[0] = 0u;
@@ -846,7 +868,16 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
     }
   }
   __syncthreads();
-  for (int i = tid; i < top_k; i += NT) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
+  if (pt_lds) {
+    const uint32_t mask = (1u << page_bits) - 1u;
+    for (int i = tid; i < top_k; i += NT) {
+      const int32_t p = i < (int)total ? (int32_t)sel[i] : -1;
+      out.page[i] = p >= 0 ? (int32_t)(((uint32_t)ptc[(uint32_t)p >> page_bits] << page_bits) | ((uint32_t)p & mask)) : -1;
+      if (out.raw) out.raw[i] = p;
+    }
+  } else {
+    for (int i = tid; i < top_k; i += NT) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
+  }
 }
 
 __global__ void topk_to_physical_kernel(const int32_t* __restrict__ topk, int64_t topk_stride,
