@@ -322,6 +322,11 @@ sparse_mla_kernel(const MlaParams P) {
   const int head = h_half + c32;                     // this lane's head (score columns)
   const bool head_ok = head < P.H;
 
+  // The indices of blocks 0-3 are fetched first, so that their round trip
+  // overlaps the query's (the wait for the query below covers them too).
+  if (wave == kIdxWave)
+    for (int j = 0; j < 4 && j < nblk; ++j) issue_index(P, smem, t, key_begin, j, lane);
+
   // Query B operands. Nope chunk c (dims 256d + 64c + 32h + 0..31 for lane half
   // h) as two fp8 terms q = 2^e_hi * hi + 2^e_lo * lo with one E8M0 exponent per
   // (head, 64-dim chunk): hi takes the top 4 significant bits of each bf16
@@ -395,11 +400,8 @@ sparse_mla_kernel(const MlaParams P) {
   float l_run = 0.f;                // per head c32: this lane's 8 keys of each block only
 
   const int my_dma = dma_count(wave);
-  // prologue: indices of blocks 0-3, then rows of blocks 0 and 1
-  if (wave == kIdxWave) {
-    for (int j = 0; j < 4 && j < nblk; ++j) issue_index(P, smem, t, key_begin, j, lane);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
+  // prologue: the indices of blocks 0-3 have landed (issued first, waited
+  // for with the query); then the rows of blocks 0 and 1
   barrier();
   const DmaLanes dl = dma_lanes(wave, lane);
   if (wave == kTabWave) {
