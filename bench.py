@@ -52,8 +52,9 @@ def parse_args():
     p.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample")
     p.add_argument("--copy-calib", action="store_true")
     p.add_argument("--unfused", action="store_true", help="indexer logits + top-k as two operators")
-    p.add_argument("--config", type=int, choices=[2, 3, 4], default=2,
-                   help="2: decode B=128 x 64K (the headline); 3: MTP verify, B=64, next_n=2, "
+    p.add_argument("--config", type=int, choices=[1, 2, 3, 4], default=2,
+                   help="1: sparse MLA decode alone, B=32 x 32K; 2: decode B=128 x 64K (the headline); "
+                        "3: MTP verify, B=64, next_n=2, "
                         "lognormal lengths (median 16K, clipped to 2K-128K); 4: chunked prefill, "
                         "8192 queries over a 120K cached prefix (128K keys)")
     p.add_argument("--only", choices=["fused", "indexer", "topk", "mla"], default=None,
@@ -249,6 +250,73 @@ def bench_prefill(args):
     }), flush=True)
 
 
+def bench_mla_decode(args):
+    """sparse MLA decode alone, batch 32, 128 heads, 32K
+    context, top-2048 indices per query from the config-0 generator scaled to
+    32K (distinct positions, randomly paged). One call = one layer's decode
+    attention; the key list is split so that the launch fills the CUs."""
+    import torch
+
+    from nanoengine_amd import _lib, mla_utils, ops, synth
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    B, L, H, K = 32, 32768, args.heads, args.topk
+    lens = [L] * B
+    gen = torch.Generator(device="cpu").manual_seed(args.seed)
+    bt, num_pages = synth.make_block_tables(lens, gen, dev)
+    kv = synth.make_mla_cache(num_pages, seed=args.seed, device=dev)
+    q = synth.make_mla_query(B, H, seed=args.seed, device=dev)
+    pos = synth.random_topk_positions(lens, K, seed=args.seed, device=dev)
+    idx = mla_utils.topk_indices_to_physical(pos, bt, 64)
+    scale = 192 ** -0.5
+    splits = ops.sparse_mla_num_splits(B, H, K, dev)
+    ws = torch.empty(max(ops.sparse_mla_workspace_bytes(B, H, splits), 1), dtype=torch.uint8, device=dev)
+    out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+
+    def call():
+        ops.sparse_mla_decode(q, kv, idx, scale, out=out, lse=lse, num_splits=splits, workspace=ws)
+
+    for _ in range(max(1, args.warmup)):
+        call()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    valid = int((idx >= 0).sum().item())
+    nbytes = valid * 656 + B * H * 576 * 2 + B * H * 512 * 2 + B * H * 4 + B * K * 4
+    flops = 2.0 * H * (576 + 512) * valid
+    gbs = nbytes / (us * 1e-6) / 1e9
+    print(json.dumps({
+        "metric": METRIC, "value": round(B / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "us_per_step": round(ms * 1e3, 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8+bf16",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 1: sparse MLA decode alone, one layer", "batch": B,
+                   "context_len": L, "index_topk": K, "mla_heads": H, "mla_dims": "576/512", "page_size": 64,
+                   "kv_cache": "fp8 656 B/token", "num_splits": splits, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "sparse_mla_kernel (+ split combine)", "bytes_per_launch": nbytes,
+                     "avg_launch_us": round(us, 2)},
+        "stages": {"sparse_mla_decode": {"us": round(us, 2), "bytes": nbytes, "GBps": round(gbs, 1),
+                                         "bf16_mfma_frac": round(flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                         "num_splits": splits}},
+        "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -260,6 +328,9 @@ def main():
         return
     if args.config == 4:
         bench_prefill(args)
+        return
+    if args.config == 1:
+        bench_mla_decode(args)
         return
 
     import torch
