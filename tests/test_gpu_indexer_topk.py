@@ -90,3 +90,16 @@ def test_workspace_and_argument_checks(cuda):
     with pytest.raises(RuntimeError, match="workspace"):
         ops.indexer_topk(inp.q_fp8.view(1, 1, 64, 128), inp.cache, inp.weights, cl, inp.block_tables, max_ctx,
                          2048, out, workspace=torch.empty(16, dtype=torch.uint8, device="cuda"))
+
+
+def test_fused_large_batch_takes_the_per_workgroup_filter(cuda):
+    """Batches above 8192 entries do not fit the persistent filter pass's LDS
+    page prefix and take the one-workgroup-per-24-pages filter instead; the
+    selection is still exactly topk_transform over indexer_logits."""
+    B, L, k = 8200, 2100, 2048
+    print(f"fused large batch B={B} L={L}", flush=True)
+    inp, cl, max_ctx = _inputs([L] * B, 1, seed=8200)
+    e_phys, e_logi = _unfused(inp, cl, max_ctx, k, 1)
+    g_phys, g_logi = _fused(inp, cl, max_ctx, k, 1)
+    assert np.array_equal(g_logi, e_logi)
+    assert np.array_equal(g_phys, e_phys)
