@@ -449,6 +449,61 @@ constexpr int kRegMaxLen = kRegThreads * kRegPerThread;  // 65536
 // Position of register slot i of thread t (slot i = element i%4 of float4 chunk i/4).
 __device__ __forceinline__ int reg_pos(int t, int i) { return 4 * kRegThreads * (i >> 2) + 4 * t + (i & 3); }
 
+// Exact selection of the `remain` largest of the n composites in list 0 of
+// LDS (hi = key - t_key, lo = (2^18 - 1) - position, so every composite is
+// distinct and equal keys favour the lower position): radix levels of 12
+// bits from the top of the nb + 18 bit composite, nb = bit length of the
+// largest hi (`hmax`), so that the digits spread over the candidates' own
+// range. Marks the selected positions in the (cleared) LDS bitmap. All NT
+// threads call it after a barrier; it ends with one.
+template <int NT>
+__device__ void composite_select(TopkSmem& s, uint32_t n, uint32_t remain, uint32_t hmax) {
+  const int tid = threadIdx.x;
+  const int nb = 32 - __clz(hmax);  // bits of the key part (0: all equal)
+  const int total_bits = nb + 18;
+  const int nlev = (total_bits + 11) / 12;
+  auto digit = [&](uint32_t h, uint32_t p, int L) {
+    const uint64_t c = ((uint64_t)h << 18) | p;
+    const int top = total_bits - 12 * L;
+    const int lo_b = max(top - 12, 0);
+    return (uint32_t)((c >> lo_b) & ((1ull << (top - lo_b)) - 1ull));
+  };
+  int cur = 0;
+  for (int L = 0; L < nlev; ++L) {
+    const int top = total_bits - 12 * L;
+    const int nbins = 1 << (top - max(top - 12, 0));
+    const int nxt = cur ^ 1;
+    // list_count[cur] (the length of this level's list) was read by every
+    // thread before the previous barrier; list_count[nxt] is free
+    for (int i = tid; i < nbins; i += NT) s.hist[i] = 0u;
+    if (tid == 0) s.list_count[nxt] = 0u;
+    __syncthreads();
+    for (uint32_t e = tid; e < n; e += NT) atomicAdd(&s.hist[digit(s.list_key[cur][e], s.list_pos[cur][e], L)], 1u);
+    __syncthreads();
+    find_threshold<NT>(s.hist, s.wave_sum, nbins, remain, &s.tb, &s.above, &s.eq);
+    const uint32_t tb = s.tb, above = s.above, eq = s.eq;
+    remain -= above;
+    const bool last = (eq == remain) || L == nlev - 1;
+    for (uint32_t e = tid; e < n; e += NT) {
+      const uint32_t h = s.list_key[cur][e], p = s.list_pos[cur][e];
+      const uint32_t d = digit(h, p, L);
+      if (d > tb || (last && d == tb)) {
+        const uint32_t pos = kIdxMax - p;
+        atomicOr(&s.bitmap[pos >> 5], 1u << (pos & 31));
+      } else if (!last && d == tb) {
+        const uint32_t slot = atomicAdd(&s.list_count[nxt], 1u);
+        s.list_key[nxt][slot] = h;
+        s.list_pos[nxt][slot] = p;
+      }
+    }
+    __syncthreads();
+    if (last) break;
+    n = s.list_count[nxt];
+    cur = nxt;
+    __syncthreads();  // every thread has read the next level's length
+  }
+}
+
 __global__ void __launch_bounds__(kRegThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const int32_t* __restrict__ page_table,
                     int64_t pt_stride, uint32_t page_bits, int32_t* __restrict__ out_page,
@@ -494,32 +549,64 @@ topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const i
   if (tid < 2) s.list_count[tid] = 0u;
   __syncthreads();
 
-  // ---- 1. threshold from the sample (slots 0, 8, 16, ...)
-  uint32_t my_samples = 0;
+  // ---- 1. threshold from the sample (slots 0, 8, 16, ...): a key at or
+  // below the sample's rank-r key, from two 1024-bin histogram levels over the
+  // sample's own [min, max] key range (binning raw order keys would put the
+  // sample into the few bins its sign and exponent span, and the LDS atomics
+  // would serialise)
+  uint32_t my_samples = 0, kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
   for (int m = 0; m < kRegPerThread / 8; ++m)
     if (key[8 * m]) {
-      atomicAdd(&s.hist[key[8 * m] >> 20], 1u);
       ++my_samples;
+      kmin = min(kmin, key[8 * m]);
+      kmax = max(kmax, key[8 * m]);
     }
+  const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    kmin = min(kmin, (uint32_t)__shfl_xor(kmin, off, 64));
+    kmax = max(kmax, (uint32_t)__shfl_xor(kmax, off, 64));
+  }
+  if (lane == 0) {
+    s.list_count[0] = 0u;
+    s.bitmap[kBitmapWords - 1 - wave] = kmin;  // scratch words far past any row of <= 64K positions
+    s.bitmap[kBitmapWords - 1 - NT / 64 - wave] = kmax;
+  }
   uint32_t nsample = 0;
   (void)block_exclusive_scan<NT>(s.wave_sum, my_samples, &nsample);
   __syncthreads();
+#pragma unroll
+  for (int w2 = 0; w2 < NT / 64; ++w2) {
+    kmin = min(kmin, s.bitmap[kBitmapWords - 1 - w2]);
+    kmax = max(kmax, s.bitmap[kBitmapWords - 1 - NT / 64 - w2]);
+  }
   const float fk = (float)nsample / (float)len * (float)top_k;
   const uint32_t r = (uint32_t)(fk + 4.f * sqrtf(fk) + 8.f);
   uint32_t t_key = 1u;  // every real key is >= 0x007fffff
   if (r < nsample) {
-    find_threshold<NT>(s.hist, s.wave_sum, 4096, r, &s.tb, &s.above, &s.eq);
-    const uint32_t tb0 = s.tb, rem0 = r - s.above;
-    __syncthreads();
-    for (int i = tid; i < 1024; i += NT) s.hist[i] = 0u;
-    __syncthreads();
+    const int shift = max(0, 32 - (int)__clz(kmax - kmin) - 10);
 #pragma unroll
     for (int m = 0; m < kRegPerThread / 8; ++m)
-      if (key[8 * m] && (key[8 * m] >> 20) == tb0) atomicAdd(&s.hist[(key[8 * m] >> 10) & 1023u], 1u);
+      if (key[8 * m]) atomicAdd(&s.hist[(key[8 * m] - kmin) >> shift], 1u);
     __syncthreads();
-    find_threshold<NT>(s.hist, s.wave_sum, 1024, rem0, &s.tb, &s.above, &s.eq);
-    t_key = max((tb0 << 20) | (s.tb << 10), 1u);
+    find_threshold<NT>(s.hist, s.wave_sum, 1024, r, &s.tb, &s.above, &s.eq);
+    const uint32_t tb0 = s.tb, rem0 = r - s.above;
+    t_key = kmin + (tb0 << shift);
+    if (shift > 0) {
+      const int shift2 = max(0, shift - 10);
+      __syncthreads();
+      for (int i = tid; i < 1024; i += NT) s.hist[i] = 0u;
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < kRegPerThread / 8; ++m)
+        if (key[8 * m] && ((key[8 * m] - kmin) >> shift) == tb0)
+          atomicAdd(&s.hist[((key[8 * m] - kmin) >> shift2) & 1023u], 1u);
+      __syncthreads();
+      find_threshold<NT>(s.hist, s.wave_sum, 1024, rem0, &s.tb, &s.above, &s.eq);
+      t_key += s.tb << shift2;
+    }
+    t_key = max(t_key, 1u);
   }
 
   // ---- 2. candidates >= t, written in thread order after one block scan; a
@@ -549,6 +636,26 @@ topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const i
   }
   const uint32_t cand = total_cand;
   const bool listed = cand >= (uint32_t)top_k && cand <= (uint32_t)kListCap;
+  if (listed) {
+    // ---- 3. exact select over the list: composites in place, their max
+    __syncthreads();  // the list is written
+    uint32_t mx = 0;
+    for (uint32_t e = tid; e < cand; e += NT) {
+      const uint32_t h = s.list_key[0][e] - t_key;
+      s.list_key[0][e] = h;
+      s.list_pos[0][e] = kIdxMax - s.list_pos[0][e];
+      mx = max(mx, h);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor(mx, off, 64));
+    if (lane == 0) s.wave_sum[wave] = mx;
+    __syncthreads();
+    mx = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < NT / 64; ++w2) mx = max(mx, s.wave_sum[w2]);
+    __syncthreads();  // wave_sum is read before composite_select reuses it
+    composite_select<NT>(s, cand, (uint32_t)top_k, mx);
+  } else {
   for (int i = tid; i < kHistBins; i += NT) s.hist[i] = 0u;
   __syncthreads();
   if (listed) {
@@ -618,6 +725,8 @@ topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const i
       cur = nxt;
       list_n = s.list_count[cur];
     }
+  }
+
   }
 
   // ---- 4. compaction in position order (two words per thread) and output
