@@ -53,6 +53,7 @@ def _fused(inp, cl, max_ctx, k, n):
     ([65536, 40000, 100, 5000], 1, 2048),
     ([20000, 70000, 3000], 2, 2048),              # MTP verify rows
     ([9000, 5000, 300], 1, 512),
+    ([262144, 3000], 1, 2048),                    # the longest row: its page table does not fit in LDS
 ])
 def test_fused_matches_indexer_then_topk(cuda, lens, n, k):
     inp, cl, max_ctx = _inputs(lens, n, seed=sum(lens) + n + k)
