@@ -11,9 +11,15 @@
 // the head weights are applied on the fp32 accumulators, and a 3-shuffle
 // butterfly finishes the head sum so that lane l ends up owning token l of the
 // page: the logits row segment and the per-token scales are then one
-// coalesced 256-byte load/store each. Each wave keeps two pages in flight
-// (three rotating register buffers) so that HBM latency overlaps compute.
-// The page primitives live in indexer_page.h.
+// coalesced 256-byte load/store each. Rotating register page buffers keep
+// pages in flight while one is multiplied. The page primitives live in
+// indexer_page.h.
+//
+// Launches: indexer_logits_kernel (one workgroup per 24 pages of a row) writes
+// the logits (the fp8_paged_mqa_logits operator), samples 16 pages per row for
+// the fused path's score threshold, or filters (batches above the persistent
+// kernel's limit); indexer_filter_kernel is the fused path's persistent filter
+// pass (one contiguous page range per wave, per-wave candidate staging).
 #include <algorithm>
 #include <type_traits>
 

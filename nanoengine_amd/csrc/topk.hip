@@ -7,7 +7,9 @@
 // positions (NaN ranks as -inf). Digits are 12/10/10 bits of the score key and
 // 9/9 bits of the inverted position.
 //
-// One call is three launches on the caller's stream:
+// Rows of at most 64K positions take one launch (topk_onepass_kernel: the
+// row in registers, a 1/8 sample for the threshold, the candidates listed in
+// LDS). Longer or ragged rows take three launches on the caller's stream:
 //   1. threshold (one workgroup per row): a 1/8 sample of the row (contiguous
 //      1024-element chunks, one in eight) gives, by a two-digit radix on the
 //      sample, a score threshold t with about k + 4 sqrt(k) elements expected
@@ -23,7 +25,11 @@
 //      needs no bound at all. The selected positions are marked in an LDS
 //      bitmap, compacted with one block prefix scan (ascending order, so the
 //      output is deterministic) and written with the page translation.
-// No global sort, no bounded candidate buffer on the exact path.
+// No global sort, no bounded candidate buffer on the exact path. The list
+// selects (one-launch kernel, the fused indexer's topk_list_kernel) radix over
+// [ key - t : nb bits ][ (2^18-1) - position : 18 bits ] instead, nb the bit
+// length of the largest key - t, so that their digits spread over the
+// candidates' own range.
 #include "dsa_common.h"
 #include "indexer_page.h"
 #include "../../include/dsa_amd.h"
