@@ -67,6 +67,8 @@ constexpr int idx_threads() { return MODE == kIdxSample ? sample_threads<NQ>() :
 constexpr int kSampleBinBits = 10;                              // threshold histogram of the sample
 constexpr int kSampleBins = 1 << kSampleBinBits;
 struct IdxSampleLds {
+  uint8_t q[2][kIdxHeads * kIdxHeadDim];  // the row's query (staged once for all waves)
+  float w[2][kIdxHeads];
   float logit[2][kSamplePages * kIdxPageTokens];
   uint32_t hist[kSampleBins];
   uint32_t wave_sum[2 * 16];
@@ -170,17 +172,13 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
   // Query heads as MFMA A operands: tile (j, ht) row i = head ht*16 + i.
   v8i qa[NQ][4];
   float w[NQ][4][4];
+  auto load_q = [&](const uint8_t* qrows, const float* wrows) {
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    const uint8_t* qb = q + ((int64_t)(b * NQ + j) * kIdxHeads) * kIdxHeadDim;
-    const float* wb = weights + (int64_t)(b * NQ + j) * kIdxHeads;
-#pragma unroll
-    for (int ht = 0; ht < 4; ++ht) {
-      qa[j][ht] = load32B(qb + (ht * 16 + (lane & 15)) * kIdxHeadDim + (lane >> 4) * 32);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) w[j][ht][r] = wb[ht * 16 + (lane >> 4) * 4 + r];
-    }
-  }
+    for (int j = 0; j < NQ; ++j)
+      load_query(qrows + j * kIdxHeads * kIdxHeadDim, wrows + j * kIdxHeads, lane, qa[j], w[j]);
+  };
+  if constexpr (MODE != kIdxSample)
+    load_q(q + ((int64_t)b * NQ * kIdxHeads) * kIdxHeadDim, weights + (int64_t)b * NQ * kIdxHeads);
 
   // Three page buffers rotate so that two pages are in flight while one is
   // being multiplied; the wave's virtual pages are vp_begin + NW*i.
@@ -200,6 +198,19 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
 #pragma unroll
     for (int i = 0; i < PPW; ++i)
       if (valid(i)) load_page(pb[i], page_ptr(i), lane);
+    // The row's query and head weights are read from L2 once per workgroup
+    // and staged in LDS, not once per wave: this pass is bound by each CU's
+    // read rate, and 16 copies of the query would double its bytes.
+    IdxSampleLds& sq = *reinterpret_cast<IdxSampleLds*>(&lds_mem);
+    {
+      const uint8_t* qsrc = q + ((int64_t)b * NQ * kIdxHeads) * kIdxHeadDim;
+      for (int e = 16 * (int)threadIdx.x; e < NQ * kIdxHeads * kIdxHeadDim; e += 16 * NT)
+        *reinterpret_cast<v4i*>(&sq.q[0][0] + e) = *reinterpret_cast<const v4i*>(qsrc + e);
+      for (int e = threadIdx.x; e < NQ * kIdxHeads; e += NT)
+        (&sq.w[0][0])[e] = weights[(int64_t)b * NQ * kIdxHeads + e];
+    }
+    __syncthreads();
+    load_q(&sq.q[0][0], &sq.w[0][0]);
 #pragma unroll
     for (int i = 0; i < PPW; ++i)
       if (valid(i)) compute(pb[i], i);
