@@ -104,3 +104,16 @@ def test_fused_large_batch_takes_the_per_workgroup_filter(cuda):
     g_phys, g_logi = _fused(inp, cl, max_ctx, k, 1)
     assert np.array_equal(g_logi, e_logi)
     assert np.array_equal(g_phys, e_phys)
+
+
+def test_fused_max_context_below_some_rows(cuda):
+    """max_context_len = 6000 (not a page multiple) with rows of 7000 and 9000
+    tokens: every stage clamps a row to max_context_len, as the unfused
+    operators do (the logits stop at max_context_len)."""
+    print("fused max_context below rows", flush=True)
+    inp, cl, _ = _inputs([7000, 5000, 9000, 2500], 1, seed=6000)
+    max_ctx, k = 6000, 2048
+    e_phys, e_logi = _unfused(inp, cl, max_ctx, k, 1)
+    g_phys, g_logi = _fused(inp, cl, max_ctx, k, 1)
+    assert np.array_equal(g_logi, e_logi)
+    assert np.array_equal(g_phys, e_phys)
