@@ -83,37 +83,74 @@ def copy_calib():
     print(json.dumps({"copy_bytes": n, "launches": 5}))
 
 
-def cpu_baseline(inp, kv, q_mla, lens, sample, scale, topk):
-    """Times the numpy oracle of the full step for `sample` sequences."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(inp, kv, q_mla, lens, sample, scale, topk, step, reps=3):
+    """Times the numpy oracle of the full step (indexer logits, exact top-k with
+    page translation, sparse MLA) on `sample` sequences spread over the batch,
+    on every host core: one warm-up, then `reps` timed repetitions, median.
+    Then checks the GPU step's outputs for the same rows against it (logits,
+    top-k, physical slots, o, LSE) and returns (baseline, parity report)."""
     import numpy as np
     import torch
     from threadpoolctl import threadpool_limits
 
     import oracle as O
+    from oracle import step_check as SC
+    from nanoengine_amd import ops
 
-    cores = min(os.cpu_count() or 1, 16)
-    bt_all = inp.block_tables[:sample].cpu().numpy()
-    used = np.unique(bt_all.reshape(-1))
-    # the sample's pages, renumbered densely (same bytes, smaller arrays)
-    remap = np.full(int(bt_all.max()) + 1, -1, np.int64)
-    remap[used] = np.arange(used.size)
-    bt = remap[bt_all].astype(np.int32)
-    idx_cache = inp.cache[torch.from_numpy(used).to(inp.cache.device)].cpu().numpy()
-    kv_rows = kv[torch.from_numpy(used).to(kv.device)].contiguous().reshape(-1, 656).cpu().numpy()
-    q_idx = inp.q_fp8[:sample].cpu().numpy().reshape(sample, 1, 64, 128)
-    w = inp.weights[:sample].cpu().numpy()
-    qm = q_mla[:sample].float().cpu().numpy()
-    ctx = np.asarray(lens[:sample], dtype=np.int32).reshape(sample, 1)
-    max_ctx = bt.shape[1] * 64
+    cores = os.cpu_count() or 1
+    B = len(lens)
+    rows = SC.spread_rows(B, sample)
+    S = len(rows)
+    max_ctx = inp.block_tables.shape[1] * 64
+    # the GPU side of the parity check: the step's last outputs, plus the
+    # standalone logits operator for the same inputs
+    seq = torch.as_tensor(lens, dtype=torch.int32, device=inp.cache.device)
+    logits = ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1),
+                                inp.block_tables, max_ctx)
+    torch.cuda.synchronize()
+    data = SC.sample_from_device(rows, q_idx_fp8=inp.q_fp8, weights=inp.weights, cache=inp.cache, lens=lens,
+                                 block_tables=inp.block_tables, q_mla=q_mla, kv=kv, logits=logits,
+                                 logical=step.logical, physical=step.physical, o=step.out, lse=step.lse)
+    del logits
+    used, bt = SC.localize_pages(data["bt_global"], data["ctx"])
+    kv_rows = kv[torch.as_tensor(used, dtype=torch.long, device=kv.device)].contiguous().reshape(-1, 656).cpu().numpy()
+    ctx = data["ctx"].reshape(S, 1)
+
+    def oracle_step():
+        lg = O.indexer_logits(data["q_idx"], data["idx_pages"], data["weights"], ctx, bt, max_ctx)
+        page, _ = O.topk_transform(lg, ctx.reshape(-1), bt, 64, topk)
+        O.sparse_mla_decode(data["q_mla"], kv_rows, page, scale)
+        return lg
+
+    times = []
     with threadpool_limits(limits=cores):
-        t0 = time.perf_counter()
-        logits = O.indexer_logits(q_idx, idx_cache, w, ctx, bt, max_ctx)
-        page, raw = O.topk_transform(logits, ctx.reshape(-1), bt, 64, topk)
-        O.sparse_mla_decode(qm, kv_rows, page, scale)
-        dt = time.perf_counter() - t0
-    return {"value": sample / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{sample} of {len(lens)} sequences of the same workload (numpy oracle: indexer "
-                      f"logits + exact top-{topk} + transform + sparse MLA), {dt:.1f} s"}
+        exp_logits = oracle_step()          # warm-up
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            oracle_step()
+            times.append(time.perf_counter() - t0)
+        rep = SC.check_step_rows(**data, sm_scale=scale, topk=topk, exp_logits=exp_logits)
+    dt = sorted(times)[len(times) // 2]
+    base = {"value": round(S / dt, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"{S} of {B} sequences spread over the batch (rows {rows.tolist()}), same workload: "
+                      f"numpy oracle of indexer logits + exact top-{topk} + transform + sparse MLA; "
+                      f"median of {reps} timed runs after 1 warm-up, {dt:.2f} s each "
+                      f"(runs: {', '.join(f'{t:.2f}' for t in times)})"}
+    rep = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in rep.items()}
+    rep["rows"] = rows.tolist()
+    return base, rep
 
 
 def prologue_stages(T, dev, seed, reps=50):
@@ -474,9 +511,9 @@ def main():
 
     stages["outside_step"] = prologue_stages(B * n, dev, args.seed)
 
-    cpu = None
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(inp, kv, q_mla, lens, min(args.cpu_sample, B), scale, K)
+        cpu, parity = cpu_baseline(inp, kv, q_mla, lens, min(args.cpu_sample, B), scale, K, step)
 
     print(json.dumps({
         "metric": METRIC, "value": round(B * n / (ms_per_step * 1e-3), 1), "unit": "tokens/s",
@@ -491,8 +528,11 @@ def main():
                    "indexer_head_dim": 128, "mla_heads": H, "mla_dims": "576/512", "page_size": 64,
                    "kv_cache": "fp8 656 B/token (block stride 65 rows)", "indexer_cache": "fp8 132 B/token",
                    "parallelism": "single GPU"},
-        "roofline": roofline, "stages": stages, "cpu_baseline": cpu,
+        "roofline": roofline, "stages": stages, "cpu_baseline": cpu, "parity": parity,
     }), flush=True)
+    if parity is not None and not parity["ok"]:
+        print(f"PARITY FAILURE: the GPU step's sampled rows do not match the oracle: {parity}", file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

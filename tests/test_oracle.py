@@ -292,3 +292,48 @@ def test_sparse_mla_prefill_matches_torch_and_decode_oracle():
     np.testing.assert_allclose(o1 * np.exp(l1 - m)[..., None] + o2 * np.exp(l2 - m)[..., None], o, atol=1e-5)
     o0, m0, l0 = O.sparse_mla_prefill(q, kv_deq, np.full((3, 32), -1, np.int32), scale)
     assert np.all(o0 == 0) and np.all(np.isneginf(l0)) and np.all(np.isneginf(m0))
+
+
+def test_step_check_catches_wrong_outputs():
+    """The sampled-row step checker passes the oracle's own outputs and fails
+    each plausible mistake: a shifted physical slot, a swapped selected
+    position, a perturbed logit, a perturbed o."""
+    from oracle import step_check as SC
+    rng = np.random.default_rng(3)
+    S, L, P, H, K = 2, 1200, 64, 4, 512
+    npg = (L + P - 1) // P
+    bt = rng.permutation(3 * npg)[:S * npg].reshape(S, npg).astype(np.int32)
+    used, btl = SC.localize_pages(bt, np.full(S, L), P)
+    assert np.array_equal(used[btl], bt)
+    codes = rng.integers(0, 0x7e, size=(used.size, P * 128), dtype=np.uint8)
+    scales = np.full((used.size, P), 0.5, np.float32).view(np.uint8)
+    pages = np.concatenate([codes, scales], axis=1)
+    q = rng.integers(0, 0x7e, size=(S, 1, 64, 128), dtype=np.uint8)
+    w = rng.standard_normal((S, 64)).astype(np.float32) * 0.01
+    ctx = np.full(S, L, np.int32)
+    logits = O.indexer_logits(q, pages, w, ctx.reshape(S, 1), btl, npg * P, P)
+    phys, raw = O.topk_transform(logits, ctx, bt, P, K)
+    qm = rng.standard_normal((S, H, 576)).astype(np.float32)
+    kv_sel = O.quantize_mla_rows(rng.standard_normal((S * K, 576)).astype(np.float32)).reshape(S, K, 656)
+    o = np.zeros((S, H, 512), np.float32)
+    lse = np.zeros((S, H), np.float32)
+    for r in range(S):
+        eo, el = O.sparse_mla_decode(qm[r:r + 1], kv_sel[r], np.arange(K)[None], 0.1)
+        o[r], lse[r] = eo[0], el[0]
+    base = dict(q_idx=q, idx_pages=pages, weights=w, ctx=ctx, bt_local=btl, bt_global=bt, max_ctx=npg * P,
+                gpu_logits=logits.copy(), gpu_logical=raw.copy(), gpu_physical=phys.copy(), q_mla=qm,
+                kv_sel=kv_sel, gpu_o=o.copy(), gpu_lse=lse.copy(), sm_scale=0.1, topk=K, page_size=P)
+    assert SC.check_step_rows(**base)["ok"]
+    bad = dict(base, gpu_physical=phys + 1)
+    assert not SC.check_step_rows(**bad)["ok"]
+    unsel = np.setdiff1d(np.arange(L), raw[0])[0]
+    lg2 = raw.copy()
+    lg2[0, 0] = unsel
+    lg2[0] = np.sort(lg2[0])
+    assert not SC.check_step_rows(**dict(base, gpu_logical=lg2))["ok"]
+    lgt = logits.copy()
+    lgt[1, 5] *= 1.01
+    assert not SC.check_step_rows(**dict(base, gpu_logits=lgt))["ok"]
+    o2 = o.copy()
+    o2[1, 2, 3] += 0.05
+    assert not SC.check_step_rows(**dict(base, gpu_o=o2))["ok"]
