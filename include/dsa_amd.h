@@ -87,6 +87,9 @@ DSA_API size_t dsa_indexer_topk_workspace_bytes(int batch, int next_n, int64_t m
  *   out_physical [batch*next_n, top_k] int32 cache slots
  *                block_tables[row / next_n, pos / 64] * 64 + pos % 64, -1 padded
  *   out_logical  [batch*next_n, top_k] int32 token positions (may be NULL)
+ * The translation goes through the indexer's own block_tables at the indexer's
+ * page size (page_size == 64): a caller whose MLA cache uses another block size
+ * must translate with dsa_topk_to_physical instead.
  * Selection, order (ascending position), ties (lowest positions) and padding are
  * those of dsa_topk_transform over dsa_indexer_logits' logits, exactly.
  * Launch sequence on `stream`: logits of 16 sampled pages per row -> per-row
@@ -141,6 +144,21 @@ DSA_API int dsa_topk_transform(const float* scores, int64_t score_stride,
                                int64_t page_table_stride, int32_t* out_page,
                                int32_t* out_raw, int batch, int64_t max_len,
                                int page_size, int top_k, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/* The portable selection tail of the decode indexer (no page translation):
+ * row r selects the top_k largest logits among positions [0, context_lens[r]),
+ * where a logit that is not finite or has |x| >= 1e30 ranks as -inf; writes
+ * the positions in ascending order, then pads with -1. Ties (including the
+ * -inf ones) go to the lowest positions. top_k in {512, 2048}; workspace as
+ * for dsa_topk_transform.
+ * Replaces the non-translating branch of Indexer.forward: masked_fill of
+ * t >= ctx, torch.where(isfinite & |x| < 1e30), torch.topk, indices >= ctx
+ * -> -1 and the -1 padding
+ * (dlengine/runtime/layers/backends/dsa/indexer/lightning.py:1468-1492). */
+DSA_API int dsa_indexer_select(const float* logits, int64_t logits_stride,
+                               const int32_t* context_lens, int32_t* out, int rows,
+                               int64_t max_len, int top_k, void* workspace,
                                size_t workspace_bytes, void* stream);
 
 /* Ragged exact top-k: row b selects among scores[b, row_starts[b] +

@@ -146,6 +146,13 @@ struct RowIn {
   const int32_t* seq_lens;
   const int32_t* row_starts;
   int64_t max_len;
+  // 1: scores that are not finite or have |x| >= 1e30 rank as -inf (the
+  // portable selection tail of the indexer, lightning.py:1474-1478); 0: only
+  // NaN does (topk_transform, topk.cuh).
+  int mask_extreme;
+  __device__ __forceinline__ uint32_t key(float x) const {
+    return order_key(mask_extreme && !(fabsf(x) < 1e30f) ? -__builtin_inff() : x);
+  }
   __device__ __forceinline__ int len(int b) const {
     int64_t l = seq_lens[b];
     return (int)(l < 0 ? 0 : (l > max_len ? max_len : l));
@@ -188,7 +195,7 @@ topk_threshold_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int pos = (c0 + c) * kStride + e * kAuxThreads + tid;
-        if (c0 + c < nchunks && pos < len) atomicAdd(&hist[order_key(x[c][e]) >> 20], 1u);
+        if (c0 + c < nchunks && pos < len) atomicAdd(&hist[in.key(x[c][e]) >> 20], 1u);
       }
   }
   uint32_t nsample = 0;
@@ -208,7 +215,7 @@ topk_threshold_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
       for (int e = 0; e < 4; ++e) {
         const int pos = c * kStride + e * kAuxThreads + tid;
         if (pos < len) {
-          const uint32_t k = order_key(row[pos]);  // second look at the sample: L2 hits
+          const uint32_t k = in.key(row[pos]);  // second look at the sample: L2 hits
           if ((k >> 20) == tb0) atomicAdd(&hist[(k >> 10) & 1023u], 1u);
         }
       }
@@ -262,7 +269,7 @@ topk_gather_kernel(const RowIn in, int top_k, RowWs* __restrict__ ws) {
       if (pred) {
         const uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
         if (slot < kGatherLdsCap) {
-          s_key[slot] = order_key(x[j]);
+          s_key[slot] = in.key(x[j]);
           s_pos[slot] = (uint32_t)pos;
         }
       }
@@ -341,7 +348,7 @@ __device__ void finish_row(TopkSmem& s, const RowIn& in, RowWs* __restrict__ ws,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int i = base + j * kTopkThreads + tid;
-        if (i < len) atomicAdd(&s.hist[order_key(x[j]) >> 20], 1u);
+        if (i < len) atomicAdd(&s.hist[in.key(x[j]) >> 20], 1u);
       }
     }
   }
@@ -388,7 +395,7 @@ __device__ void finish_row(TopkSmem& s, const RowIn& in, RowWs* __restrict__ ws,
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int i = base + j * kTopkThreads + tid;
-          const uint32_t key = order_key(x[j]);
+          const uint32_t key = in.key(x[j]);
           if (i < len && in_bucket(level, key, (uint32_t)i, thr)) visit(key, (uint32_t)i);
         }
       }
@@ -546,7 +553,7 @@ topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const i
     const int p = 4 * kRegThreads * j + 4 * tid;
     const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(row + min(p, last)));
 #pragma unroll
-    for (int e = 0; e < 4; ++e) key[4 * j + e] = p + e < len ? order_key(v[e]) : 0u;
+    for (int e = 0; e < 4; ++e) key[4 * j + e] = p + e < len ? in.key(v[e]) : 0u;
   }
 
   const int nwords = (len + 31) >> 5;
@@ -717,7 +724,7 @@ topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const i
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int i = base + j * NT + tid;
-          const uint32_t k = order_key(x[j]);
+          const uint32_t k = in.key(x[j]);
           if (i < len && in_bucket(level, k, (uint32_t)i, thr)) visit(k, (uint32_t)i);
         }
       }
@@ -1103,6 +1110,23 @@ int dsa_topk_transform(const float* scores, int64_t score_stride, const int32_t*
   return launch_topk(in, batch, nullptr, page_table, page_table_stride, bits, out_page,
                      page_table ? out_raw : nullptr, top_k, workspace, workspace_bytes, (hipStream_t)stream,
                      "dsa_topk_transform");
+}
+
+int dsa_indexer_select(const float* logits, int64_t logits_stride, const int32_t* context_lens,
+                       int32_t* out, int rows, int64_t max_len, int top_k, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  using namespace dsa;
+  if (top_k != 512 && top_k != 2048)
+    return set_error(kInvalidArgument, "top_k must be 512 or 2048, got %d", top_k);
+  if (rows < 0 || max_len < 0 || (rows > 0 && (!logits || !context_lens || !out)))
+    return set_error(kInvalidArgument, "dsa_indexer_select: bad arguments");
+  if (max_len > kTopkMaxLen)
+    return set_error(kUnsupported, "logits rows longer than %d are not supported (got %lld)",
+                     kTopkMaxLen, (long long)max_len);
+  if (rows == 0) return kOk;
+  const RowIn in{logits, logits_stride, context_lens, nullptr, max_len, 1};
+  return launch_topk(in, rows, nullptr, nullptr, 0, 0u, out, nullptr, top_k, workspace, workspace_bytes,
+                     (hipStream_t)stream, "dsa_indexer_select");
 }
 
 int dsa_topk_transform_ragged(const float* scores, int64_t score_stride, const int32_t* seq_lens,

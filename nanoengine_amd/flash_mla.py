@@ -15,20 +15,27 @@ from . import ops
 
 
 class SparseMlaSchedule:
-    """Opaque per-shape schedule: the split count and a reusable workspace."""
+    """Opaque schedule: the split count and a workspace per shape. Every
+    shape's workspace is kept for the schedule's lifetime, because a HIP graph
+    captured at one shape holds that workspace's address: freeing it when the
+    shape changes would let later replays write their split partials over
+    whatever the allocator put there next."""
 
     def __init__(self) -> None:
         self.num_splits: int | None = None
         self.workspace: torch.Tensor | None = None
         self.key: tuple | None = None
+        self._by_key: dict = {}
 
     def prepare(self, num_tokens: int, num_heads: int, topk: int, device: torch.device) -> None:
         key = (num_tokens, num_heads, topk, device)
         if self.key == key:
             return
-        self.num_splits = ops.sparse_mla_num_splits(num_tokens, num_heads, topk, device)
-        need = ops.sparse_mla_workspace_bytes(num_tokens, num_heads, self.num_splits)
-        self.workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+        if key not in self._by_key:
+            splits = ops.sparse_mla_num_splits(num_tokens, num_heads, topk, device)
+            need = ops.sparse_mla_workspace_bytes(num_tokens, num_heads, splits)
+            self._by_key[key] = (splits, torch.empty(max(need, 1), dtype=torch.uint8, device=device))
+        self.num_splits, self.workspace = self._by_key[key]
         self.key = key
 
 

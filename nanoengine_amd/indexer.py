@@ -112,10 +112,29 @@ def indexer_decode_topk(q_fp8: torch.Tensor, weights: torch.Tensor, kv_cache_buf
         deepseek_v4.topk_transform(logits, seq_lens, page_tables, physical, topk_page_size, index_topk,
                                    logical)
         return logical, physical
-    if index_topk not in (512, 2048):
-        raise ValueError(f"top_k must be 512 or 2048, got {index_topk}")
-    ops.topk_transform_raw(logits, seq_lens, logical, index_topk)
-    return logical
+    if index_topk in (512, 2048):
+        ops.indexer_select(logits, seq_lens, logical, index_topk)
+        return logical
+    return _select_other_k(logits, seq_lens, index_topk, logical)
+
+
+def _select_other_k(logits: torch.Tensor, seq_lens: torch.Tensor, index_topk: int,
+                    out: torch.Tensor) -> torch.Tensor:
+    """Top-k sizes the HIP select does not instantiate (the model uses 2048):
+    the same masking rules with torch's own GPU sort, then ascending order and
+    -1 padding as the HIP select writes them (lightning.py:1468-1492)."""
+    width = logits.shape[1]
+    pos = torch.arange(width, device=logits.device)
+    ok = (pos[None, :] < seq_lens[:, None]) & torch.isfinite(logits) & (logits.abs() < 1e30)
+    masked = torch.where(ok, logits, torch.full_like(logits, float("-inf")))
+    k = min(index_topk, width)
+    # a stable descending sort breaks ties by the lowest position, as the HIP select does
+    idx = torch.sort(masked, dim=-1, descending=True, stable=True).indices[:, :k]
+    idx = torch.where(idx < seq_lens[:, None], idx, torch.full_like(idx, width))
+    idx = idx.sort(dim=-1).values.to(torch.int32)
+    out.fill_(-1)
+    out[:, :k] = torch.where(idx < width, idx, torch.full_like(idx, -1))
+    return out
 
 
 def _logits_into(q4, kv_cache, weights, ctx, bt, max_context_len, out):

@@ -171,6 +171,9 @@ def _event_array(events):
 
 # --------------------------------------------------------------------------- top-k
 _TOPK_WS: dict = {}
+# buffers replaced by a larger one: kept alive because a captured HIP graph may
+# still hold their addresses (never freed before the process ends)
+_TOPK_WS_RETIRED: list = []
 
 
 def topk_workspace_bytes(batch: int) -> int:
@@ -179,11 +182,14 @@ def topk_workspace_bytes(batch: int) -> int:
 
 def topk_workspace(batch: int, device: torch.device) -> torch.Tensor:
     """Workspace for the top-k entry points, cached per (device, stream) and
-    grown on demand; calls on one stream are ordered, so sharing is safe."""
+    grown on demand; calls on one stream are ordered, so sharing is safe. A
+    buffer that is outgrown stays allocated (graphs may have captured it)."""
     need = int(_lib.load().dsa_topk_workspace_bytes(batch))
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _TOPK_WS.get(key)
     if ws is None or ws.numel() < need:
+        if ws is not None:
+            _TOPK_WS_RETIRED.append(ws)
         ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
         _TOPK_WS[key] = ws
     return ws
@@ -241,6 +247,27 @@ def topk_transform_raw(scores: torch.Tensor, seq_lens: torch.Tensor, out_indices
     _lib.call("dsa_topk_transform", scores.data_ptr(), scores.stride(0), seq_lens.data_ptr(), None, 0,
               out_indices.data_ptr(), None, B, scores.shape[1], 1, int(top_k), *_ws_args(workspace),
               _stream(dev))
+
+
+def indexer_select(logits: torch.Tensor, context_lens: torch.Tensor, out_indices: torch.Tensor,
+                   top_k: int, workspace=None) -> None:
+    """The portable selection tail of the decode indexer: exact top-k positions
+    among [0, context_lens[r]) with non-finite and |x| >= 1e30 logits ranked as
+    -inf, ascending, -1 padded (``dsa_indexer_select``)."""
+    if top_k not in (512, 2048):
+        raise ValueError(f"top_k must be 512 or 2048, got {top_k}")
+    _require(logits.dim() == 2 and logits.dtype == torch.float32 and logits.stride(1) == 1,
+             "logits must be f32 [rows, S] with unit column stride")
+    R = logits.shape[0]
+    _require(context_lens.dtype == torch.int32 and tuple(context_lens.shape) == (R,)
+             and context_lens.is_contiguous(), "context_lens must be contiguous int32 [rows]")
+    _require(out_indices.dtype == torch.int32 and tuple(out_indices.shape) == (R, top_k)
+             and out_indices.is_contiguous(), f"out_indices must be contiguous int32 [{R}, {top_k}]")
+    dev = _check_cuda(logits, context_lens, out_indices)
+    if workspace is None:
+        workspace = topk_workspace(R, dev)
+    _lib.call("dsa_indexer_select", logits.data_ptr(), logits.stride(0), context_lens.data_ptr(),
+              out_indices.data_ptr(), R, logits.shape[1], int(top_k), *_ws_args(workspace), _stream(dev))
 
 
 def topk_transform_ragged(scores: torch.Tensor, seq_lens: torch.Tensor, row_starts: torch.Tensor,

@@ -23,6 +23,9 @@ class DsaDecodeStep:
         self.batch, self.next_n, self.max_ctx = batch, next_n, max_context_len
         self.num_heads, self.topk, self.page_size = num_heads, index_topk, page_size
         self.fused = fused
+        if fused and page_size != 64:
+            # the fused kernel translates through the indexer's 64-token pages
+            raise ValueError(f"the fused indexer + top-k step needs page_size 64 (the indexer page), got {page_size}")
         rows = batch * next_n
         dev = torch.device(device)
         if fused:

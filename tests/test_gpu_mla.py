@@ -144,3 +144,45 @@ def test_graph_capture_replays_match_eager(cuda):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager_o) and torch.equal(lse, eager_l)
+
+
+def test_schedule_keeps_workspaces_for_captured_graphs(cuda):
+    """One schedule captured in HIP graphs at two batch sizes (both split the
+    key list, so both use the workspace), then an eager call at a third size
+    and other allocations; both graphs must still replay to their eager
+    results (a freed workspace would be reused by the allocator)."""
+    H, K, scale = 128, 2048, 192 ** -0.5
+    sched, _ = flash_mla.get_mla_metadata()
+    cases = {}
+    for T in (2, 5):
+        q, kv, idx = _case(T, H, K, num_blocks=80, seed=40 + T)
+        assert ops.sparse_mla_num_splits(T, H, K, cuda) > 1
+        args = (q.view(T, 1, H, 576), kv, None, None, 512, sched, None, scale)
+        eager = [t.clone() for t in flash_mla.flash_mla_with_kvcache(*args, is_fp8_kvcache=True,
+                                                                        indices=idx.view(T, 1, K))]
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            flash_mla.flash_mla_with_kvcache(*args, is_fp8_kvcache=True, indices=idx.view(T, 1, K))
+            with torch.cuda.graph(g, stream=s):
+                outs = flash_mla.flash_mla_with_kvcache(*args, is_fp8_kvcache=True, indices=idx.view(T, 1, K))
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        # the graph does not keep its inputs alive: hold them for the replays
+        cases[T] = (g, outs, eager, (q, kv, idx))
+    q3, kv3, idx3 = _case(3, H, K, num_blocks=80, seed=49)
+    flash_mla.flash_mla_with_kvcache(q3.view(3, 1, H, 576), kv3, None, None, 512, sched, None, scale,
+                                     is_fp8_kvcache=True, indices=idx3.view(3, 1, K))
+    junk = [torch.full((1 << 20,), 7, dtype=torch.uint8, device=cuda) for _ in range(8)]
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for T, (g, outs, eager, _) in cases.items():
+            for t in outs:
+                t.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            for a, b in zip(outs, eager):
+                assert torch.equal(a, b), T
+    del junk

@@ -193,3 +193,35 @@ def test_sample_blind_spots_fall_back_exactly(cuda):
     e_page, e_raw = O.topk_transform(scores, lens, pt, 64, 2048)
     assert np.array_equal(raw, e_raw)
     assert np.array_equal(out, e_page)
+
+
+@pytest.mark.parametrize("width,k", [(9000, 2048), (70000, 2048), (9000, 512), (3000, 100)])
+@pytest.mark.parametrize("with_ws", [True, False])
+def test_indexer_select_masks_extreme_logits(cuda, width, k, with_ws):
+    """The indexer's portable selection tail (lightning.py:1468-1492): +inf,
+    NaN, |x| >= 1e30 rank as -inf; positions past the context are never
+    selected; compared with the oracle's indexer_decode_topk. Rows: more
+    extreme values than non-selected room (so -inf ties are selected), a row
+    shorter than k, and ordinary rows. k=100 takes the torch route."""
+    from nanoengine_amd import indexer as nidx
+    rng = np.random.default_rng(width + k)
+    R = 4
+    logits = rng.standard_normal((R, width)).astype(np.float32)
+    for r in range(R):
+        hot = rng.choice(width, size=width // 3, replace=False)
+        vals = np.array([np.inf, -np.inf, np.nan, 1e31, -1e31, 3e38, 1e30], np.float32)
+        logits[r, hot] = vals[rng.integers(0, vals.size, hot.size)]
+    logits[2, : width // 2] = np.inf      # the whole first half masked
+    ctx = np.array([width, width - 37, width // 2 + 5, min(k - 1, width)], np.int32)
+    if not with_ws and k not in (512, 2048):
+        pytest.skip("the torch route takes no workspace")
+    out = torch.empty(R, k, dtype=torch.int32, device=cuda)
+    lg = torch.from_numpy(logits).to(cuda)
+    cl = torch.from_numpy(ctx).to(cuda)
+    if k in (512, 2048):
+        ops.indexer_select(lg, cl, out, k, workspace=None if with_ws else False)
+    else:
+        nidx._select_other_k(lg, cl, k, out)
+    torch.cuda.synchronize()
+    exp = O.indexer_decode_topk(logits, ctx, k)
+    assert np.array_equal(out.cpu().numpy(), exp)

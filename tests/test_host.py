@@ -90,3 +90,11 @@ def test_gather_indexer_cache_argument_checks():
         gather_indexer_cache(cache, bt, torch.tensor([0, 5, 9]), page_size=32, head_dim=128)
     with pytest.raises(ValueError, match="contiguous 2D uint8"):
         gather_indexer_cache(cache.float(), bt, torch.tensor([0, 5, 9]), page_size=64, head_dim=128)
+
+
+def test_fused_step_rejects_non_indexer_page_size():
+    """The fused indexer + top-k translates through the indexer's 64-token
+    pages; another MLA block size must be refused, not silently mistranslated."""
+    from nanoengine_amd.pipeline import DsaDecodeStep
+    with pytest.raises(ValueError, match="page_size 64"):
+        DsaDecodeStep(2, 1, 4096, page_size=32, device="cpu", fused=True)
