@@ -146,6 +146,22 @@ DSA_API int dsa_topk_transform(const float* scores, int64_t score_stride,
                                int page_size, int top_k, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* dsa_topk_transform without a workspace argument and without any allocation:
+ * the per-row state lives in a fixed device array of the library (12.6 MB per
+ * GPU, held until the process ends), for at most 256 rows (more: status
+ * kUnsupported). Results are those of dsa_topk_transform. Calls on one GPU
+ * share that array: calls that overlap in time on one device (different
+ * streams, or different host threads without ordering) race and must not be
+ * made. The kernels reset the state they use, so no clearing is needed
+ * between calls.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (HIP graph capture, allocation-free serving loops). */
+DSA_API int dsa_topk_transform_noalloc(const float* scores, int64_t score_stride,
+                                       const int32_t* seq_lens, const int32_t* page_table,
+                                       int64_t page_table_stride, int32_t* out_page,
+                                       int32_t* out_raw, int batch, int64_t max_len,
+                                       int page_size, int top_k, void* stream);
+
 /* The portable selection tail of the decode indexer (no page translation):
  * row r selects the top_k largest logits among positions [0, context_lens[r]),
  * where a logit that is not finite or has |x| >= 1e30 ranks as -inf; writes

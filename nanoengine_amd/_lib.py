@@ -27,6 +27,8 @@ SIGNATURES = {
     "dsa_topk_workspace_bytes": (c_size_t, [c_int]),
     "dsa_topk_transform": (c_int, [_P, c_int64, _P, _P, c_int64, _P, _P, c_int, c_int64, c_int, c_int, _P,
                                    c_size_t, _P]),
+    "dsa_topk_transform_noalloc": (c_int, [_P, c_int64, _P, _P, c_int64, _P, _P, c_int, c_int64, c_int, c_int,
+                                           _P]),
     "dsa_indexer_select": (c_int, [_P, c_int64, _P, _P, c_int, c_int64, c_int, _P, c_size_t, _P]),
     "dsa_topk_transform_ragged": (c_int, [_P, c_int64, _P, _P, _P, _P, c_int, c_int64, c_int, _P, c_size_t,
                                           _P]),

@@ -30,6 +30,8 @@
 // [ key - t : nb bits ][ (2^18-1) - position : 18 bits ] instead, nb the bit
 // length of the largest key - t, so that their digits spread over the
 // candidates' own range.
+#include <mutex>
+
 #include "dsa_common.h"
 #include "indexer_page.h"
 #include "../../include/dsa_amd.h"
@@ -1040,6 +1042,36 @@ static int prepare_topk_kernel() {
 }
 
 // The launches of one selection. `workspace` NULL: the exact full path only.
+// Scratch of the no-allocation entry point: the per-row state (threshold,
+// candidate count, candidate list) of up to kNoAllocRows rows, held by every
+// GPU the library runs on until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol):
+// each device's address comes from hipGetSymbolAddress, once per device.
+constexpr int kNoAllocRows = 256;
+static __device__ __align__(256) uint8_t scratch[kNoAllocRows * sizeof(RowWs)];
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// This device's address of `scratch` (looked up on the first call with that
+// device current, then cached).
+static int device_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(kLaunchFailed, "dsa_topk_transform_noalloc: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(kLaunchFailed, "dsa_topk_transform_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return kOk;
+}
+
 static int launch_topk(const RowIn& in, int batch, const int32_t* offsets, const int32_t* page_table,
                        int64_t pt_stride, uint32_t page_bits, int32_t* out_page, int32_t* out_raw,
                        int top_k, void* workspace, size_t workspace_bytes, hipStream_t stream,
@@ -1110,6 +1142,33 @@ int dsa_topk_transform(const float* scores, int64_t score_stride, const int32_t*
   return launch_topk(in, batch, nullptr, page_table, page_table_stride, bits, out_page,
                      page_table ? out_raw : nullptr, top_k, workspace, workspace_bytes, (hipStream_t)stream,
                      "dsa_topk_transform");
+}
+
+int dsa_topk_transform_noalloc(const float* scores, int64_t score_stride, const int32_t* seq_lens,
+                               const int32_t* page_table, int64_t page_table_stride, int32_t* out_page,
+                               int32_t* out_raw, int batch, int64_t max_len, int page_size, int top_k,
+                               void* stream) {
+  using namespace dsa;
+  if (top_k != 512 && top_k != 2048)
+    return set_error(kInvalidArgument, "top_k must be 512 or 2048, got %d", top_k);
+  if (page_size <= 0 || (page_size & (page_size - 1)))
+    return set_error(kInvalidArgument, "page_size must be power of 2, got %d", page_size);
+  if (batch < 0 || max_len < 0 || (batch > 0 && (!scores || !seq_lens || !out_page)))
+    return set_error(kInvalidArgument, "dsa_topk_transform_noalloc: bad arguments");
+  if (batch > kNoAllocRows)
+    return set_error(kUnsupported, "dsa_topk_transform_noalloc: %d rows exceed the scratch maximum of %d rows",
+                     batch, kNoAllocRows);
+  if (max_len > kTopkMaxLen)
+    return set_error(kUnsupported, "score rows longer than %d are not supported (got %lld)",
+                     kTopkMaxLen, (long long)max_len);
+  if (batch == 0) return kOk;
+  void* ws = nullptr;
+  if (int rc = device_scratch(&ws)) return rc;
+  const RowIn in{scores, score_stride, seq_lens, nullptr, max_len};
+  const uint32_t bits = (uint32_t)__builtin_ctz((unsigned)page_size);
+  return launch_topk(in, batch, nullptr, page_table, page_table_stride, bits, out_page,
+                     page_table ? out_raw : nullptr, top_k, ws, (size_t)kNoAllocRows * sizeof(RowWs),
+                     (hipStream_t)stream, "dsa_topk_transform_noalloc");
 }
 
 int dsa_indexer_select(const float* logits, int64_t logits_stride, const int32_t* context_lens,
