@@ -218,6 +218,9 @@ DSA_API size_t dsa_sparse_mla_workspace_bytes(int num_tokens, int num_heads, int
  *            scales are powers of two, as the reference's writer produces
  *            (2^ceil(log2(amax/448)), fp8_utils.py:32-108) and the kernel
  *            reads them as E8M0 exponents
+ *   kv_num_blocks  blocks in the cache: a slot whose block is >= this (or a
+ *            negative slot) is skipped like -1, so a stale index never reads
+ *            outside the cache
  *   indices  [num_tokens, topk] int32 physical slots (block*kv_block_size+row),
  *            row stride idx_stride, -1 = skip
  *   out      [num_tokens, num_heads, 512] bf16, contiguous
@@ -233,7 +236,8 @@ DSA_API size_t dsa_sparse_mla_workspace_bytes(int num_tokens, int num_heads, int
  * (dlengine/runtime/layers/backends/mla/flash_mla.py:76-99). */
 DSA_API int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                           const uint8_t* kv_cache, int64_t kv_block_stride_bytes,
-                          int kv_block_size, const int32_t* indices, int64_t idx_stride,
+                          int kv_block_size, int64_t kv_num_blocks,
+                          const int32_t* indices, int64_t idx_stride,
                           int num_tokens, int num_heads, int topk, float sm_scale,
                           void* out, float* lse, int num_splits,
                           void* workspace, size_t workspace_bytes, void* stream);

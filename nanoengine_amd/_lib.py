@@ -6,10 +6,12 @@ importing an op raises. Build it with ``python -m nanoengine_amd.build``.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libdsa_amd.so"
+# DSA_AMD_LIB may name another build of the same library (a variant under test)
+LIB_PATH = Path(os.environ.get("DSA_AMD_LIB", Path(__file__).resolve().parent / "libdsa_amd.so"))
 
 # name -> (restype, argtypes); mirrors include/dsa_amd.h one to one.
 _P = c_void_p
@@ -35,8 +37,8 @@ SIGNATURES = {
     "dsa_topk_to_physical": (c_int, [_P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, c_int, _P, _P]),
     "dsa_sparse_mla_num_splits": (c_int, [c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
-    "dsa_sparse_mla_decode": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int, _P, c_int64, c_int, c_int,
-                                      c_int, c_float, _P, _P, c_int, _P, c_size_t, _P]),
+    "dsa_sparse_mla_decode": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int, c_int64, _P, c_int64, c_int,
+                                      c_int, c_int, c_float, _P, _P, c_int, _P, c_size_t, _P]),
     "dsa_mla_kv_store": (c_int, [_P, c_int64, _P, c_int, c_int, _P, c_int64, c_int, _P]),
     "dsa_indexer_k_store": (c_int, [_P, c_int64, _P, c_int, c_int, _P, c_int, _P]),
     "dsa_indexer_q_prologue": (c_int, [_P, _P, c_int64, c_float, _P, c_int64, _P, c_int, c_int, c_int, c_int, _P,

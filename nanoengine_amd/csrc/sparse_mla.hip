@@ -95,6 +95,7 @@ struct MlaParams {
   int64_t q_tok_stride, q_head_stride;
   const uint8_t* kv;
   int64_t kv_blk_stride;
+  int64_t kv_num_blocks;
   int kv_block_size;
   int kv_block_shift;  // log2(kv_block_size) when it is a power of two, else -1
   const int32_t* idx;
@@ -210,8 +211,19 @@ __device__ __forceinline__ v16f mfma_fp8_chunk(int c, v8i a, v8i b, v16f acc, in
 // pairs are loop invariants, computed once per lane (DmaLanes).
 constexpr int kTabWave = 6;  // the wave that builds the row-address table
 
+// Cache block of a physical slot.
+__device__ __forceinline__ int64_t slot_block(const MlaParams& P, int32_t slot) {
+  return P.kv_block_shift >= 0 ? (int64_t)(slot >> P.kv_block_shift) : (int64_t)(slot / P.kv_block_size);
+}
+
+// A slot is used when it is >= 0 and inside the cache; any other index
+// (-1 padding, or a stale value past the cache) is skipped.
+__device__ __forceinline__ bool slot_valid(const MlaParams& P, int32_t slot) {
+  return slot >= 0 && slot_block(P, slot) < P.kv_num_blocks;
+}
+
 __device__ __forceinline__ uint64_t row_address(const MlaParams& P, int32_t slot) {
-  if (slot < 0) return reinterpret_cast<uint64_t>(g_mla_zero_row);
+  if (!slot_valid(P, slot)) return reinterpret_cast<uint64_t>(g_mla_zero_row);
   int64_t blk, in_blk;
   if (P.kv_block_shift >= 0) {
     blk = slot >> P.kv_block_shift;
@@ -428,7 +440,7 @@ sparse_mla_kernel(const MlaParams P) {
     // tables are double-buffered by block parity.
     const uint8_t* buf = smem + (n % kNumBufs) * kBufBytes;
     const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kRingOff + (n % kRingSlots) * 256)[lane];
-    const uint64_t vmask = __ballot(slot_n >= 0);
+    const uint64_t vmask = __ballot(slot_valid(P, slot_n));
     if (wave == kIdxWave && n + 4 < nblk) issue_index(P, smem, t, key_begin, n + 4, lane);
     // row addresses of block n+2 (its indices landed before the last barrier), read after B3
     if (wave == kTabWave && n + 2 < nblk) build_addr_table(P, smem, n + 2, lane);
@@ -705,9 +717,9 @@ size_t dsa_sparse_mla_workspace_bytes(int num_tokens, int num_heads, int num_spl
 
 int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                           const uint8_t* kv_cache, int64_t kv_block_stride_bytes, int kv_block_size,
-                          const int32_t* indices, int64_t idx_stride, int num_tokens, int num_heads,
-                          int topk, float sm_scale, void* out, float* lse, int num_splits, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+                          int64_t kv_num_blocks, const int32_t* indices, int64_t idx_stride, int num_tokens,
+                          int num_heads, int topk, float sm_scale, void* out, float* lse, int num_splits,
+                          void* workspace, size_t workspace_bytes, void* stream) {
   using namespace dsa;
   if (num_tokens < 0 || num_heads <= 0 || (num_heads % 16) != 0)
     return set_error(kUnsupported, "sparse_mla: num_heads=%d must be a positive multiple of 16", num_heads);
@@ -718,6 +730,7 @@ int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_
                      (long long)kv_block_stride_bytes, kv_block_size);
   if (kv_block_stride_bytes % 16 != 0)
     return set_error(kInvalidArgument, "sparse_mla: kv block stride must be a multiple of 16 bytes");
+  if (kv_num_blocks < 0) return set_error(kInvalidArgument, "sparse_mla: kv_num_blocks < 0");
   if (num_tokens == 0) return kOk;
   if (!q || !kv_cache || !indices || !out)
     return set_error(kInvalidArgument, "sparse_mla: null pointer");
@@ -754,6 +767,7 @@ int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_
   P.kv = kv_cache;
   P.kv_blk_stride = kv_block_stride_bytes;
   P.kv_block_size = kv_block_size;
+  P.kv_num_blocks = kv_num_blocks;
   P.idx = indices;
   P.idx_stride = idx_stride;
   P.T = num_tokens;

@@ -363,7 +363,8 @@ def sparse_mla_decode(q: torch.Tensor, k_cache: torch.Tensor, indices: torch.Ten
     ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
     ws_bytes = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
     _lib.call("dsa_sparse_mla_decode", q.data_ptr(), q.stride(0), q.stride(1), _as_bytes(k_cache).data_ptr(),
-              blk_stride, block_size, indices.data_ptr(), indices.stride(0), T, H, topk, float(sm_scale),
+              blk_stride, block_size, k_cache.shape[0], indices.data_ptr(), indices.stride(0), T, H, topk,
+              float(sm_scale),
               out.data_ptr(), lse.data_ptr(), int(num_splits), ws_ptr, ws_bytes, _stream(dev))
     return out, lse
 

@@ -62,10 +62,13 @@ def test_argument_errors_return_status_without_a_device(lib):
     assert lib.dsa_indexer_logits(P, P, P, P, P, 0, 1, 1, 32, 128, 64, 64, P, 64, P) == 2
     assert lib.dsa_indexer_logits(P, P, P, P, P, 0, 1, 3, 64, 128, 64, 64, P, 64, P) == 2
     # sparse MLA: heads must be a multiple of 16, topk a multiple of 64
-    assert lib.dsa_sparse_mla_decode(P, 0, 0, P, 42640, 64, P, 0, 1, 24, 2048, ctypes.c_float(0.1), P, P, 1,
-                                     P, 0, P) == 2
-    assert lib.dsa_sparse_mla_decode(P, 0, 0, P, 42640, 64, P, 0, 1, 128, 100, ctypes.c_float(0.1), P, P, 1,
-                                     P, 0, P) == 2
+    assert lib.dsa_sparse_mla_decode(P, 0, 0, P, 42640, 64, 10, P, 0, 1, 24, 2048, ctypes.c_float(0.1), P, P,
+                                     1, P, 0, P) == 2
+    assert lib.dsa_sparse_mla_decode(P, 0, 0, P, 42640, 64, 10, P, 0, 1, 128, 100, ctypes.c_float(0.1), P, P,
+                                     1, P, 0, P) == 2
+    # a split count that does not split top-k into whole 64-row blocks
+    assert lib.dsa_sparse_mla_decode(P, 0, 0, P, 42640, 64, 10, P, 0, 1, 128, 192, ctypes.c_float(0.1), P, P,
+                                     2, P, 0, P) == 1
     # empty batches are a no-op success
     assert lib.dsa_topk_transform(P, 0, P, P, 0, P, P, 0, 0, 64, 2048, P, 0, P) == 0
     with pytest.raises(ValueError):
@@ -80,7 +83,7 @@ def test_workspace_size_queries(lib):
     assert lib.dsa_indexer_topk_workspace_bytes(128, 1, 65536) >= 128 * (16 + 8 * 6144) + 128 * 65536 * 4
     assert lib.dsa_sparse_mla_workspace_bytes(128, 128, 1) == 0
     assert lib.dsa_sparse_mla_workspace_bytes(32, 128, 4) == 4 * 32 * 128 * (512 + 1) * 4
-    # splits grow until the grid covers the CUs, in 64-row blocks of top-k
+    # splits grow until the grid (64 heads per workgroup) covers the CUs, in 64-row blocks of top-k
     assert lib.dsa_sparse_mla_num_splits(128, 128, 2048, 256) == 1
     assert lib.dsa_sparse_mla_num_splits(32, 128, 2048, 256) == 4
     assert lib.dsa_sparse_mla_num_splits(1, 16, 128, 256) == 2

@@ -94,6 +94,24 @@ def test_invalid_indices_and_empty_rows(cuda):
         assert torch.all(o[1] == 0) and torch.all(torch.isneginf(lse[1]))
 
 
+def test_slots_past_the_cache_are_skipped(cuda):
+    """A slot whose block lies past the cache (a stale index) is skipped like -1
+    rather than read out of bounds."""
+    q, kv, idx = _case(2, 128, 512, num_blocks=40, seed=5)
+    bad = idx.clone()
+    g = torch.Generator(device="cpu").manual_seed(5)
+    past = torch.rand(bad.shape, generator=g) < 0.25
+    bad[past.to(bad.device)] = 40 * 64 + 7          # block 40 of a 40-block cache
+    ref = idx.clone()
+    ref[past.to(ref.device)] = -1
+    scale = 192 ** -0.5
+    for splits in (1, 2):
+        o, lse = ops.sparse_mla_decode(q, kv, bad, scale, num_splits=splits)
+        eo, el = ops.sparse_mla_decode(q, kv, ref, scale, num_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(o, eo) and torch.equal(lse, el)
+
+
 def test_split_counts_agree(cuda):
     q, kv, idx = _case(2, 128, 2048, num_blocks=64, seed=8)
     outs = [ops.sparse_mla_decode(q, kv, idx, 0.07, num_splits=s) for s in (1, 2, 8, 32)]
