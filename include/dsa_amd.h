@@ -346,6 +346,24 @@ DSA_API int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, i
                                      void* stream);
 
 
+/* Per-query key windows of a ragged prefill batch, computed on the device.
+ *   cu_seqlens_q/_k [num_seqs + 1] int32 (cu_is_64 = 0) or int64: sequence b's
+ *              fresh queries are the last q_len of its k_len keys
+ *   ks, ke     [num_queries] int32 out: query i of sequence b scores keys
+ *              [cu_k[b], i + 1 + cu_k[b+1] - cu_q[b+1])
+ *   status     [4] int64 out: {fault bits, total keys, longest k length, most
+ *              pages (of page_size) in one sequence}; fault bit 0: cu_q or cu_k
+ *              does not start at 0, bit 1: cu_q does not end at num_queries,
+ *              bit 2: a q length < 0 or a k length < its q length (then ks/ke
+ *              are meaningless)
+ * Replaces the host-side window build of Indexer.compute_prefill_topk_paged
+ * (dlengine/runtime/layers/backends/dsa/indexer/lightning.py:1138-1206: the
+ * cu_seqlens checks and the ks/ke construction). */
+DSA_API int dsa_prefill_windows(const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64,
+                                int num_seqs, int num_queries, int page_size, int32_t* ks,
+                                int32_t* ke, int64_t* status, void* stream);
+
+
 /* Sparse MLA prefill over ragged bf16 KV rows.
  *   q          [num_tokens, num_heads, 576] bf16 (row stride q_token_stride, head
  *              stride q_head_stride elements, last dim contiguous)

@@ -218,6 +218,63 @@ mqa_logits_clean_kernel(const int32_t* __restrict__ ks, const int32_t* __restric
   }
 }
 
+
+// Per-query key windows of a ragged prefill batch, on the device. Query i of
+// sequence b (cu_q[b] <= i < cu_q[b+1]) sees the sequence's cached prefix and
+// the fresh keys up to its own: [cu_k[b], i + 1 + (cu_k[b+1] - cu_q[b+1])), the
+// causal rule of dlengine/runtime/layers/backends/dsa/indexer/lightning.py:
+// 1190-1206 written in closed form. One thread per query finds b by binary
+// search. Workgroup 0 also checks the batch and writes status[4] =
+// {fault bits, total keys, longest key length, most pages of one sequence}
+// (bit 0: cu_q or cu_k does not start at 0; bit 1: cu_q does not end at
+// num_queries; bit 2: some q length < 0 or k length < q length), so the host
+// validates with one read of 32 bytes.
+__global__ void __launch_bounds__(256)
+prefill_windows_kernel(const void* __restrict__ cu_q, const void* __restrict__ cu_k, int cu_is_64, int num_seqs,
+                       int num_queries, int page_size, int32_t* __restrict__ ks, int32_t* __restrict__ ke,
+                       int64_t* __restrict__ status) {
+  auto cu = [&](const void* p, int i) -> int64_t {
+    return cu_is_64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
+  };
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < num_queries) {
+    int lo = 0, hi = num_seqs;  // largest b < num_seqs with cu_q[b] <= i
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (cu(cu_q, mid) <= i) lo = mid; else hi = mid;
+    }
+    ks[i] = (int32_t)cu(cu_k, lo);
+    ke[i] = (int32_t)(i + 1 + cu(cu_k, lo + 1) - cu(cu_q, lo + 1));
+  }
+  if (blockIdx.x != 0) return;
+  __shared__ unsigned long long s_bits, s_maxk, s_maxp;
+  if (threadIdx.x == 0) s_bits = s_maxk = s_maxp = 0;
+  __syncthreads();
+  unsigned long long bits = 0, maxk = 0, maxp = 0;
+  for (int b = threadIdx.x; b < num_seqs; b += 256) {
+    const int64_t ql = cu(cu_q, b + 1) - cu(cu_q, b), kl = cu(cu_k, b + 1) - cu(cu_k, b);
+    if (ql < 0 || kl < ql) bits |= 4;
+    if (kl > 0) {
+      maxk = max(maxk, (unsigned long long)kl);
+      maxp = max(maxp, (unsigned long long)((kl + page_size - 1) / page_size));
+    }
+  }
+  if (threadIdx.x == 0) {
+    if (cu(cu_q, 0) != 0 || cu(cu_k, 0) != 0) bits |= 1;
+    if (cu(cu_q, num_seqs) != num_queries) bits |= 2;
+  }
+  atomicOr(&s_bits, bits);
+  atomicMax(&s_maxk, maxk);
+  atomicMax(&s_maxp, maxp);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    status[0] = (int64_t)s_bits;
+    status[1] = cu(cu_k, num_seqs);
+    status[2] = (int64_t)s_maxk;
+    status[3] = (int64_t)s_maxp;
+  }
+}
+
 }  // namespace
 }  // namespace dsa
 
@@ -257,6 +314,19 @@ int dsa_mqa_logits(const uint8_t* q, const uint8_t* kv, const float* kv_scale, c
                      weights, weights_stride, ks, ke, num_rows, num_keys, token_blocks, chunk_keys, logits,
                      logits_stride);
   return check_launch("dsa_mqa_logits");
+}
+
+int dsa_prefill_windows(const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64, int num_seqs,
+                        int num_queries, int page_size, int32_t* ks, int32_t* ke, int64_t* status, void* stream) {
+  using namespace dsa;
+  if (num_seqs < 1 || num_queries < 0 || page_size <= 0)
+    return set_error(kInvalidArgument, "dsa_prefill_windows: bad sizes");
+  if (!cu_seqlens_q || !cu_seqlens_k || !status || (num_queries > 0 && (!ks || !ke)))
+    return set_error(kInvalidArgument, "dsa_prefill_windows: null pointer");
+  const int grid = std::max(1, (num_queries + 255) / 256);
+  hipLaunchKernelGGL(prefill_windows_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, cu_seqlens_q,
+                     cu_seqlens_k, cu_is_64, num_seqs, num_queries, page_size, ks, ke, status);
+  return check_launch("dsa_prefill_windows");
 }
 
 }  // extern "C"

@@ -11,7 +11,6 @@ from __future__ import annotations
 import torch
 
 from . import deep_gemm, deepseek_v4, ops
-from .deepseek_v4 import topk_transform_ragged
 from .indexer_cache_gather import gather_indexer_cache
 
 INDEXER_QUANT_BLOCK_SIZE = 128
@@ -142,27 +141,37 @@ def _logits_into(q4, kv_cache, weights, ctx, bt, max_context_len, out):
     return ops.indexer_logits(q4, kv, weights, ctx, bt, max_context_len, out=out)
 
 
-def _prefill_mqa_chunk_rows(num_queries: int, num_keys: int, device: torch.device,
-                            max_rows: int | None = None) -> int:
-    """Query rows per ragged-logits chunk, from the memory a [rows, num_keys]
-    f32 logits tensor needs (lightning.py:381-405)."""
-    if num_queries <= 0:
-        return 0
+# Logits workspace of one prefill call: at most this fraction of the device's
+# HBM (9 GB on a 288 GB MI355X, a whole 8K x 128K chunk of f32 logits). The rows
+# of a chunk follow from it; the buffer is allocated once per call and reused.
+PREFILL_LOGITS_HBM_FRACTION = 1 / 32
+_HBM_BYTES: dict = {}
+
+
+def _prefill_chunk_rows(num_queries: int, num_keys: int, device: torch.device,
+                        query_chunk: int | None = None) -> int:
+    """Query rows per logits chunk: as many [rows, num_keys] f32 rows as fit in
+    the call's logits workspace, capped by ``query_chunk``."""
     if num_keys <= 0:
         raise ValueError("prefill Indexer requires at least one key")
-    if max_rows is not None and max_rows <= 0:
-        raise ValueError(f"max_rows must be positive, got {max_rows}")
-    rows = num_queries
-    logits_elements = num_queries * num_keys
-    if logits_elements >= 8_000_000:
-        free_mem, total_mem = torch.cuda.mem_get_info(device)
-        logits_bytes = logits_elements * 4
-        if logits_bytes * 2 > free_mem or logits_bytes > total_mem * 0.3:
-            bytes_per_row = num_keys * 4
-            rows = max(1, int((free_mem * 0.45) // bytes_per_row))
-    if max_rows is not None:
-        rows = min(rows, max_rows)
+    dev = torch.device(device)
+    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    if key not in _HBM_BYTES:
+        _HBM_BYTES[key] = torch.cuda.get_device_properties(key[1]).total_memory
+    budget = int(_HBM_BYTES[key] * PREFILL_LOGITS_HBM_FRACTION)
+    rows = max(1, budget // (4 * num_keys))
+    if query_chunk is not None:
+        rows = min(rows, query_chunk)
     return min(rows, num_queries)
+
+
+def _select_rows_descending(logits: torch.Tensor, out: torch.Tensor, top_k: int) -> None:
+    """Top-k sizes other than 2048 on window-cleaned logits: positions by
+    descending logit, non-finite picks as -1, -1 padding past the key count
+    (lightning.py:1232-1245). ``out`` arrives filled with -1."""
+    k = min(top_k, logits.shape[1])
+    vals, pos = torch.topk(logits, k, dim=-1)
+    out[:, :k] = torch.where(torch.isfinite(vals), pos.to(torch.int32), -1)
 
 
 def compute_prefill_topk_paged(q_fp8: torch.Tensor, weights: torch.Tensor, cu_seqlens_q: torch.Tensor,
@@ -180,67 +189,69 @@ def compute_prefill_topk_paged(q_fp8: torch.Tensor, weights: torch.Tensor, cu_se
     cache_buf [num_pages, page_size * 132] uint8. Returns packed global
     logical indices [num_queries, index_topk] int32 into the ragged key order
     (sequence b's keys at cu_seqlens_k[b] ...), -1 padded.
+
+    The windows and the batch checks run in one kernel (``ops.prefill_windows``);
+    the host reads its 32-byte status once, which is the call's only
+    synchronisation. The paged keys are gathered to ragged order once, then
+    the logits go chunk by chunk through one reused workspace, each chunk
+    followed by its top-k (the fused exact select for 2048).
     """
     if query_chunk is not None and query_chunk <= 0:
         raise ValueError(f"query_chunk must be positive, got {query_chunk}")
     if cu_seqlens_q.shape != cu_seqlens_k.shape:
         raise RuntimeError("cu_seqlens_q/cu_seqlens_k shape mismatch: "
                            f"{cu_seqlens_q.shape} vs {cu_seqlens_k.shape}")
+    dev = q_fp8.device
     num_queries = q_fp8.shape[0]
-    indices = torch.full((num_queries, index_topk), -1, dtype=torch.int32, device=q_fp8.device)
+    indices = torch.full((num_queries, index_topk), -1, dtype=torch.int32, device=dev)
     if num_queries == 0:
         return indices
-    head_dim = q_fp8.shape[-1]
     num_seqs = cu_seqlens_q.numel() - 1
     if block_table.shape[0] != num_seqs:
         raise RuntimeError(f"block_table/cu_seqlens batch mismatch: {block_table.shape[0]} vs {num_seqs}")
-    q_first = int(cu_seqlens_q[0].item())
-    k_first = int(cu_seqlens_k[0].item())
-    q_total = int(cu_seqlens_q[-1].item())
-    if q_first != 0 or k_first != 0:
+
+    cu_dtype = torch.int64 if torch.int64 in (cu_seqlens_q.dtype, cu_seqlens_k.dtype) else torch.int32
+    cu_q = cu_seqlens_q.to(cu_dtype).contiguous()
+    cu_k = cu_seqlens_k.to(cu_dtype).contiguous()
+    windows = torch.empty(2, num_queries, dtype=torch.int32, device=dev)
+    ks, ke = windows[0], windows[1]
+    status = torch.empty(4, dtype=torch.int64, device=dev)
+    ops.prefill_windows(cu_q, cu_k, num_queries, page_size, ks, ke, status)
+    faults, total_k, max_seqlen_k, max_pages = status.tolist()
+    if faults & 1:
         raise RuntimeError("ragged Indexer cu_seqlens must start at zero")
-    if q_total != num_queries:
+    if faults & 2:
+        q_total = int(cu_q[-1])
         raise RuntimeError(f"cu_seqlens_q does not cover the packed queries: {q_total} vs {num_queries}")
-    q_lens = (cu_seqlens_q[1:] - cu_seqlens_q[:-1]).to(torch.int32)
-    k_lens = (cu_seqlens_k[1:] - cu_seqlens_k[:-1]).to(torch.int32)
-    if bool(torch.any(q_lens < 0).item()) or bool(torch.any(k_lens < q_lens).item()):
+    if faults & 4:
         raise RuntimeError("Invalid prefill ragged lengths: K length must cover every Q length")
-    used_pages = torch.div(k_lens + page_size - 1, page_size, rounding_mode="floor")
-    if int(used_pages.max().item()) > block_table.shape[1]:
+    if max_pages > block_table.shape[1]:
         raise RuntimeError("Indexer block table is too short for the longest sequence")
 
-    total_k = int(cu_seqlens_k[-1].item())
-    max_seqlen_k = int(k_lens.max().item())
-    key_bytes, scale_bytes = gather_indexer_cache(cache_buf, block_table, cu_seqlens_k, page_size=page_size,
-                                                  head_dim=head_dim, total_k=total_k, max_seqlen_k=max_seqlen_k)
-    kv_fp8 = (key_bytes.view(torch.float8_e4m3fn), scale_bytes.view(torch.float32).reshape(-1))
+    key_bytes, scale_bytes = gather_indexer_cache(cache_buf, block_table, cu_k, page_size=page_size,
+                                                  head_dim=q_fp8.shape[-1], total_k=total_k,
+                                                  max_seqlen_k=max_seqlen_k)
+    keys = key_bytes.view(torch.float8_e4m3fn)
+    key_scales = scale_bytes.view(torch.float32).reshape(-1)
 
-    q_to_seq = torch.repeat_interleave(torch.arange(num_seqs, dtype=torch.int64, device=q_fp8.device),
-                                       q_lens.to(torch.int64), output_size=num_queries)
-    q_starts = cu_seqlens_q[:-1].index_select(0, q_to_seq).to(torch.int32)
-    k_starts = cu_seqlens_k[:-1].index_select(0, q_to_seq).to(torch.int32)
-    cached_lens = (k_lens - q_lens).index_select(0, q_to_seq)
-    local_q = torch.arange(num_queries, dtype=torch.int32, device=q_fp8.device) - q_starts
-    ks = k_starts.contiguous()
-    ke = (ks + cached_lens + local_q + 1).contiguous()
-
-    chunk_rows = _prefill_mqa_chunk_rows(num_queries, total_k, q_fp8.device, max_rows=query_chunk)
-    use_fused_topk = index_topk == 2048
-    valid_lens = (ke - ks).contiguous()
-    for start in range(0, num_queries, chunk_rows):
-        end = min(start + chunk_rows, num_queries)
-        logits = deep_gemm.fp8_mqa_logits(q_fp8[start:end], kv_fp8, weights[start:end], ks[start:end],
-                                          ke[start:end], clean_logits=not use_fused_topk)
-        if use_fused_topk:
-            topk_transform_ragged(logits, valid_lens[start:end], ks[start:end], ks[start:end],
-                                  indices[start:end], index_topk)
+    fused = index_topk == 2048
+    rows = _prefill_chunk_rows(num_queries, total_k, dev, query_chunk)
+    workspace = torch.empty(rows, total_k, dtype=torch.float32, device=dev)
+    lens = (ke - ks) if fused else None
+    for r0 in range(0, num_queries, rows):
+        r1 = min(r0 + rows, num_queries)
+        logits = workspace[:r1 - r0]
+        _score_chunk(q_fp8[r0:r1], keys, key_scales, weights[r0:r1], ks[r0:r1], ke[r0:r1], logits,
+                     clean=not fused)
+        if fused:
+            # positions come back relative to the window start; adding ks makes them global
+            ops.topk_transform_ragged(logits, lens[r0:r1], ks[r0:r1], ks[r0:r1], indices[r0:r1], index_topk)
         else:
-            actual_topk = min(index_topk, total_k)
-            top_values, logical = logits.topk(actual_topk, dim=-1)
-            logical = logical.to(torch.int32).masked_fill_(~torch.isfinite(top_values), -1)
-            if actual_topk < index_topk:
-                logical = torch.nn.functional.pad(logical, (0, index_topk - actual_topk), value=-1)
-            indices[start:end] = logical
-            del top_values, logical
-        del logits
+            _select_rows_descending(logits, indices[r0:r1], index_topk)
     return indices
+
+
+def _score_chunk(q, keys, key_scales, weights, ks, ke, out, clean: bool) -> None:
+    """Ragged logits of one chunk of queries into ``out`` (the weighted-ReLU
+    fp8 MQA score of lightning.py:116-162, every key j in [ks, ke))."""
+    ops.mqa_logits(q, keys, key_scales, weights, ks, ke, out, clean_logits=clean)

@@ -487,6 +487,27 @@ def mqa_logits(q_fp8: torch.Tensor, kv_fp8: torch.Tensor, kv_scale: torch.Tensor
               out.data_ptr(), out.stride(0), out.shape[1], int(bool(clean_logits)), _stream(dev))
 
 
+def prefill_windows(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, num_queries: int, page_size: int,
+                    ks: torch.Tensor, ke: torch.Tensor, status: torch.Tensor) -> None:
+    """Per-query key windows [ks, ke) of a ragged prefill batch and the batch's
+    status {fault bits, total keys, longest k length, most pages} (see
+    dsa_prefill_windows), on the device."""
+    _require(cu_seqlens_q.dtype == cu_seqlens_k.dtype and cu_seqlens_q.dtype in (torch.int32, torch.int64),
+             "cu_seqlens_q/_k must share one dtype, int32 or int64", ValueError)
+    _require(cu_seqlens_q.dim() == 1 and cu_seqlens_q.shape == cu_seqlens_k.shape and cu_seqlens_q.numel() >= 2
+             and cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous(),
+             "cu_seqlens_q/_k must be contiguous [num_seqs + 1], num_seqs >= 1", ValueError)
+    for t in (ks, ke):
+        _require(t.dtype == torch.int32 and tuple(t.shape) == (num_queries,) and t.is_contiguous(),
+                 "ks/ke must be contiguous int32 [num_queries]", ValueError)
+    _require(status.dtype == torch.int64 and status.numel() == 4 and status.is_contiguous(),
+             "status must be contiguous int64 [4]", ValueError)
+    dev = _check_cuda(cu_seqlens_q, cu_seqlens_k, ks, ke, status)
+    _lib.call("dsa_prefill_windows", cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+              int(cu_seqlens_q.dtype == torch.int64), cu_seqlens_q.numel() - 1, int(num_queries), int(page_size),
+              ks.data_ptr(), ke.data_ptr(), status.data_ptr(), _stream(dev))
+
+
 def gather_indexer_cache(cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_k: torch.Tensor,
                          page_size: int, total_k: int, key_out: torch.Tensor, scale_out: torch.Tensor) -> None:
     """Paged indexer pages -> ragged keys [total_k, 128] and scale bytes [total_k, 4]

@@ -67,17 +67,16 @@ def test_driver_multi_seq_causal_ranges_and_chunks(cuda, monkeypatch):
         gather_calls.append((cu_k.clone(), kw))
         return real_gather(cache, page_table, cu_k, **kw)
 
-    def fake_logits(q, kv, weights, ks, ke, clean_logits=False):
-        assert clean_logits is True
+    def fake_logits(q, keys, key_scales, weights, ks, ke, out, clean):
+        assert clean is True
         seen.append((ks.tolist(), ke.tolist()))
-        total_k = kv[0].shape[0]
-        logits = torch.arange(total_k, dtype=torch.float32, device=cuda).expand(q.shape[0], -1).clone()
+        total_k = keys.shape[0]
+        out.copy_(torch.arange(total_k, dtype=torch.float32, device=cuda).expand(q.shape[0], -1))
         cols = torch.arange(total_k, device=cuda).unsqueeze(0)
-        logits.masked_fill_((cols < ks[:, None]) | (cols >= ke[:, None]), -torch.inf)
-        return logits
+        out.masked_fill_((cols < ks[:, None]) | (cols >= ke[:, None]), -torch.inf)
 
     monkeypatch.setattr(indexer_module, "gather_indexer_cache", spy_gather)
-    monkeypatch.setattr(indexer_module.deep_gemm, "fp8_mqa_logits", fake_logits)
+    monkeypatch.setattr(indexer_module, "_score_chunk", fake_logits)
     cache = torch.zeros(6, 4 * 132, dtype=torch.uint8, device=cuda)
     q = torch.zeros(5, 64, 128, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)
     w = torch.ones(5, 64, dtype=torch.float32, device=cuda)
@@ -108,6 +107,37 @@ def test_driver_validation(cuda):
                                                                             device=cuda), bt, cache, page_size=4)
     with pytest.raises(ValueError, match="query_chunk must be positive"):
         indexer_module.compute_prefill_topk_paged(q, w, cu_q, cu_q, bt, cache, page_size=4, query_chunk=0)
+    with pytest.raises(RuntimeError, match="must start at zero"):
+        indexer_module.compute_prefill_topk_paged(q, w, torch.tensor([1, 2, 5], dtype=torch.int32, device=cuda),
+                                                  cu_q + 1, bt, cache, page_size=4)
+    with pytest.raises(RuntimeError, match="does not cover the packed queries: 4 vs 5"):
+        indexer_module.compute_prefill_topk_paged(q, w, torch.tensor([0, 2, 4], dtype=torch.int32, device=cuda),
+                                                  torch.tensor([0, 5, 9], dtype=torch.int32, device=cuda), bt,
+                                                  cache, page_size=4)
+
+
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_prefill_windows_match_oracle(cuda, dtype):
+    """The device-side windows equal the oracle's causal [ks, ke) on a ragged
+    batch with empty sequences and prefix-free ones; the status carries the
+    totals the gather sizes from."""
+    print(f"prefill windows {dtype}", flush=True)
+    rng = np.random.default_rng(3)
+    q_lens = rng.integers(0, 300, 37)
+    q_lens[[0, 5, 36]] = 0
+    k_lens = q_lens + rng.integers(0, 5000, 37)
+    k_lens[7] = q_lens[7]                       # no cached prefix
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)])
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)])
+    nq = int(cu_q[-1])
+    ks = torch.empty(nq, dtype=torch.int32, device=cuda)
+    ke = torch.empty_like(ks)
+    status = torch.empty(4, dtype=torch.int64, device=cuda)
+    ops.prefill_windows(torch.from_numpy(cu_q).to(cuda, dtype), torch.from_numpy(cu_k).to(cuda, dtype), nq, 64,
+                        ks, ke, status)
+    eks, eke = O.prefill_ks_ke(cu_q, cu_k)
+    assert np.array_equal(ks.cpu().numpy(), eks) and np.array_equal(ke.cpu().numpy(), eke)
+    assert status.tolist() == [0, int(cu_k[-1]), int(k_lens.max()), int(((k_lens + 63) // 64).max())]
 
 
 def test_driver_long_rows_fused_topk_is_exact(cuda, monkeypatch):
@@ -116,14 +146,13 @@ def test_driver_long_rows_fused_topk_is_exact(cuda, monkeypatch):
     print("prefill driver long rows", flush=True)
     seen = []
 
-    def fake_logits(q, kv, weights, ks, ke, clean_logits=False):
-        assert clean_logits is False
+    def fake_logits(q, keys, key_scales, weights, ks, ke, out, clean):
+        assert clean is False
         g = torch.Generator(device=cuda).manual_seed(7)
-        logits = torch.randn(q.shape[0], kv[0].shape[0], dtype=torch.float32, device=cuda, generator=g)
-        seen.append(logits)
-        return logits
+        out.copy_(torch.randn(q.shape[0], keys.shape[0], dtype=torch.float32, device=cuda, generator=g))
+        seen.append(out.clone())
 
-    monkeypatch.setattr(indexer_module.deep_gemm, "fp8_mqa_logits", fake_logits)
+    monkeypatch.setattr(indexer_module, "_score_chunk", fake_logits)
     cache = torch.zeros(1, 64 * 132, dtype=torch.uint8, device=cuda)
     q = torch.zeros(2, 64, 128, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)
     w = torch.ones(2, 64, dtype=torch.float32, device=cuda)

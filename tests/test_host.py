@@ -66,18 +66,20 @@ def test_golden_fixture_reproduces_from_the_oracle():
         assert set(ref.tolist()) == set(raw[b, :k].tolist())
 
 
-def test_prefill_mqa_chunk_rows_respects_available_memory(monkeypatch):
-    """Chunk sizing from free memory (lightning.py:381-405; the reference's
-    tests/test_indexer_prefill.py:228-237 cases)."""
-    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda _device: (1_000_000, 10_000_000))
-    dev = torch.device("cuda")
-    assert indexer._prefill_mqa_chunk_rows(100, 100_000, dev) == 1
-    assert indexer._prefill_mqa_chunk_rows(100, 100_000, dev, max_rows=7) == 1
-    assert indexer._prefill_mqa_chunk_rows(10, 100, dev) == 10
-    assert indexer._prefill_mqa_chunk_rows(10, 100, dev, max_rows=3) == 3
-    with pytest.raises(ValueError):
-        indexer._prefill_mqa_chunk_rows(10, 0, dev)
-    assert indexer._prefill_mqa_chunk_rows(0, 10, dev) == 0
+def test_prefill_chunk_rows_follow_the_logits_workspace(monkeypatch):
+    """Chunk rows = the [rows, num_keys] f32 logits that fit in the call's
+    workspace (a fixed fraction of the device's HBM), capped by query_chunk."""
+    class Props:
+        total_memory = 32 * 4 * 100_000 * 10      # a workspace of 10 rows of 100K keys
+    monkeypatch.setattr(torch.cuda, "get_device_properties", lambda _i: Props())
+    monkeypatch.setattr(indexer, "_HBM_BYTES", {})
+    dev = torch.device("cuda", 0)
+    assert indexer._prefill_chunk_rows(100, 100_000, dev) == 10
+    assert indexer._prefill_chunk_rows(100, 100_000, dev, query_chunk=7) == 7
+    assert indexer._prefill_chunk_rows(4, 100_000, dev) == 4
+    assert indexer._prefill_chunk_rows(100, 10_000_000, dev) == 1   # never below one row
+    with pytest.raises(ValueError, match="at least one key"):
+        indexer._prefill_chunk_rows(10, 0, dev)
 
 
 def test_gather_indexer_cache_argument_checks():
