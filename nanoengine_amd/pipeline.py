@@ -15,6 +15,7 @@ from __future__ import annotations
 import torch
 
 from . import ops
+from .state import IndexerTopKState
 
 
 class DsaDecodeStep:
@@ -53,12 +54,28 @@ class DsaDecodeStep:
 
     def __call__(self, q_idx_fp8: torch.Tensor, weights: torch.Tensor, indexer_cache: torch.Tensor,
                  seq_lens: torch.Tensor, block_tables: torch.Tensor, page_tables: torch.Tensor,
-                 q_mla: torch.Tensor, kv_cache: torch.Tensor, sm_scale: float):
+                 q_mla: torch.Tensor, kv_cache: torch.Tensor, sm_scale: float, *,
+                 layer_idx: int | None = None, indexer_state: IndexerTopKState | None = None,
+                 shared: bool = False):
         """q_idx_fp8 [B*n, 64, 128] fp8; weights [B*n, 64] f32; indexer_cache
         [pages, 8448] uint8; seq_lens [B*n] int32 per-query lengths;
         block_tables [B, M] int32; page_tables [B*n, M] int32 (block_tables
         repeated per query token); q_mla [B*n, H, 576] bf16; kv_cache
-        [blocks, 64, 1, 656] fp8 bytes. Returns (o, lse, logical, physical)."""
+        [blocks, 64, 1, 656] fp8 bytes. Returns (o, lse, logical, physical).
+
+        With an ``indexer_state``, a full layer (``shared=False``) publishes its
+        (logical, physical) pair under ``layer_idx``; a shared layer
+        (``shared=True``) runs no indexer and attends over the published pair,
+        which must match this batch's shape (deepseek_v2.py:1865-1950). The
+        indexer inputs are not read on a shared layer and may be None."""
+        if shared:
+            if indexer_state is None:
+                raise ValueError("a shared indexer layer needs the indexer_state of a preceding full layer")
+            logical, physical = indexer_state.require(layer_idx, self.batch * self.next_n, self.topk,
+                                                      require_physical=True)
+            ops.sparse_mla_decode(q_mla, kv_cache, physical, sm_scale, out=self.out, lse=self.lse,
+                                  num_splits=self.num_splits, workspace=self.workspace)
+            return self.out, self.lse, logical, physical
         B, n = self.batch, self.next_n
         q4 = q_idx_fp8.view(B, n, *q_idx_fp8.shape[1:])
         if self.fused:
@@ -69,6 +86,8 @@ class DsaDecodeStep:
                                out=self.logits)
             ops.topk_transform(self.logits, seq_lens, page_tables, self.physical, self.page_size, self.topk,
                                self.logical, workspace=self.topk_workspace)
+        if indexer_state is not None:
+            indexer_state.publish(layer_idx, self.logical, self.physical)
         ops.sparse_mla_decode(q_mla, kv_cache, self.physical, sm_scale, out=self.out, lse=self.lse,
                               num_splits=self.num_splits, workspace=self.workspace)
         return self.out, self.lse, self.logical, self.physical

@@ -72,3 +72,39 @@ def test_graph_capture_of_the_fused_step(cuda):
         torch.cuda.synchronize()
         for a, b in zip(outs, eager):
             assert torch.equal(a, b)
+
+
+def test_shared_layer_reuses_the_published_topk(cuda):
+    """A full layer publishes its (logical, physical) pair; the next shared
+    layer runs no indexer (its indexer inputs are None) and attends over
+    exactly those slots: its output is bit-identical to sparse MLA over the
+    published physical indices with the shared layer's own query and cache."""
+    from nanoengine_amd import ops
+    from nanoengine_amd.state import IndexerTopKState
+    lens, n, H = [5000, 65536, 1200, 30000], 1, 128
+    inp, kv, q, max_ctx = _step_inputs(lens, n, H, seed=23)
+    step = DsaDecodeStep(len(lens), n, max_ctx, num_heads=H, device=cuda)
+    state = IndexerTopKState()
+    seq = step.expand_lens(inp.context_lens)
+    pt = inp.block_tables.repeat_interleave(n, dim=0).contiguous()
+    _, _, logical, physical = step(inp.q_fp8, inp.weights, inp.cache, seq, inp.block_tables, pt, q, kv,
+                                   192 ** -0.5, layer_idx=2, indexer_state=state)
+    published = (logical.clone(), physical.clone())
+    assert state.source_layer == 2 and state.logical_indices is logical
+    kv3 = synth.make_mla_cache(kv.shape[0], seed=99, device="cuda")
+    q3 = synth.make_mla_query(len(lens) * n, H, seed=99, device="cuda")
+    o, lse, l3, p3 = step(None, None, None, None, None, None, q3, kv3, 192 ** -0.5, layer_idx=3,
+                          indexer_state=state, shared=True)
+    o, lse = o.clone(), lse.clone()
+    eo, else_ = ops.sparse_mla_decode(q3, kv3, published[1], 192 ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(l3, published[0]) and torch.equal(p3, published[1])
+    assert torch.equal(o, eo) and torch.equal(lse, else_)
+    # a shared layer with nothing published, or at another batch shape, is refused
+    with pytest.raises(RuntimeError, match="no TopK"):
+        step(None, None, None, None, None, None, q3, kv3, 0.1, layer_idx=3, indexer_state=IndexerTopKState(),
+             shared=True)
+    small = IndexerTopKState()
+    small.publish(2, published[0][:2], published[1][:2])
+    with pytest.raises(RuntimeError, match="stale TopK shape"):
+        step(None, None, None, None, None, None, q3, kv3, 0.1, layer_idx=3, indexer_state=small, shared=True)
