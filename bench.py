@@ -57,7 +57,7 @@ def parse_args():
                         "3: MTP verify, B=64, next_n=2, "
                         "lognormal lengths (median 16K, clipped to 2K-128K); 4: chunked prefill, "
                         "8192 queries over a 120K cached prefix (128K keys)")
-    p.add_argument("--only", choices=["fused", "indexer", "topk", "mla"], default=None,
+    p.add_argument("--only", choices=["fused", "indexer", "topk", "mla", "logits", "kv"], default=None,
                    help="profiling aid: launch only this stage in the timed loop (no JSON line)")
     return p.parse_args()
 
@@ -193,14 +193,93 @@ def prologue_stages(T, dev, seed, reps=50):
     return out
 
 
+def cpu_baseline_prefill(host, rows, scale, topk, gpu, reps=3):
+    """The numpy oracle of config 4 on the host cores: the per-chunk work (the
+    indexer key gather and the MLA key assembly from the fp8 cache) once, and
+    the per-query work (ragged logits, exact top-k, sparse MLA prefill) for the
+    sampled query rows; one warm-up, `reps` timed runs, medians. The reported
+    rate is the chunk's queries over (per-chunk time + queries x per-query
+    time). Then checks the GPU's outputs for the same rows against it: logits
+    within each row's window, the top-k of the GPU's own logits, the assembled
+    keys (bit-exact) and the MLA output."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    import oracle as O
+
+    cores = os.cpu_count() or 1
+    QN, KN = host["QN"], host["KN"]
+    S = len(rows)
+    ks = np.zeros(S, np.int32)
+    ke = (KN - QN + 1 + rows).astype(np.int32)
+
+    def chunk_part():
+        keys, kscale = O.gather_indexer_cache(host["idx_cache"], host["bt"], host["cu_k"])
+        kv = O.assemble_prefill_kv(host["mla_rows"], 64, host["bt"], host["cu_q"], host["cu_k"], host["fresh"])
+        return keys, kscale, kv
+
+    def row_part(keys, kscale, kv):
+        lg = O.mqa_logits(host["q8"], keys, kscale, host["w"], ks, ke, clean_logits=True)
+        idx = O.topk_transform_ragged(lg, ke - ks, ks, ks, topk)
+        o, mx, lse = O.sparse_mla_prefill(host["q_mla"], kv, idx, scale)
+        return lg, idx, o, lse
+
+    t_chunk, t_rows = [], []
+    with threadpool_limits(limits=cores):
+        keys, kscale, kv = chunk_part()                 # warm-up
+        exp = row_part(keys, kscale, kv)
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            keys, kscale, kv = chunk_part()
+            t1 = time.perf_counter()
+            row_part(keys, kscale, kv)
+            t2 = time.perf_counter()
+            t_chunk.append(t1 - t0)
+            t_rows.append(t2 - t1)
+        # parity: the GPU's rows against the oracle
+        lg_exp = exp[0]
+        rel = 0.0
+        for r in range(S):
+            a, e = ks[r], ke[r]
+            g, x = gpu["logits"][r, a:e].astype(np.float64), lg_exp[r, a:e].astype(np.float64)
+            rel = max(rel, float(np.abs(g - x).max() / max(np.abs(x).max(), np.sqrt(np.mean(x * x)), 1e-30)))
+        own = O.topk_transform_ragged(np.where(np.arange(KN)[None, :] < ke[:, None], gpu["logits"], -np.inf),
+                                      ke - ks, ks, ks, topk)
+        topk_equal = all(set(own[r][own[r] >= 0].tolist()) == set(gpu["idx"][r][gpu["idx"][r] >= 0].tolist())
+                         for r in range(S))
+        used = np.unique(gpu["idx"][gpu["idx"] >= 0])
+        kv_equal = bool(np.array_equal(gpu["kv_rows"], kv[used]))
+        o_exp, _, lse_exp = O.sparse_mla_prefill(host["q_mla"], kv, gpu["idx"], scale)
+    o_err = float(np.abs(gpu["o"] - o_exp).max())
+    lse_err = float(np.abs(gpu["lse"] - lse_exp).max())
+    tc, tr = sorted(t_chunk)[len(t_chunk) // 2], sorted(t_rows)[len(t_rows) // 2]
+    per_query = tr / S
+    value = QN / (tc + QN * per_query)
+    base = {"value": round(value, 3), "unit": "tokens/s", "cores": cores, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"per-chunk work (indexer key gather + MLA key assembly from the fp8 cache, {KN} keys) "
+                      f"in full, {tc:.2f} s; per-query work (ragged logits, exact top-{topk}, sparse MLA "
+                      f"prefill) on {S} of {QN} queries spread over the chunk (rows {rows.tolist()}), "
+                      f"{tr:.2f} s; medians of {reps} timed runs after 1 warm-up; value = {QN} / "
+                      f"({tc:.2f} + {QN} x {per_query:.3f}) s"}
+    ok = rel <= 1e-3 and topk_equal and kv_equal and o_err <= 2e-2 and lse_err <= 1e-3
+    parity = {"rows": rows.tolist(), "logits_max_rel_err": round(rel, 6), "topk_equal_on_gpu_logits": topk_equal,
+              "kv_rows_bit_exact": kv_equal, "o_max_abs_err": round(o_err, 6), "lse_max_abs_err": round(lse_err, 6),
+              "ok": bool(ok)}
+    return base, parity
+
+
 def bench_prefill(args):
     """one 8192-token chunk over a 122880-token cached prefix
     (131072 keys in all). Stages, each timed with HIP events on the launch
-    stream over `steps` repetitions: the paged-to-ragged key gather, the ragged
-    fp8 MQA logits [8192 x 131072] (causal windows), and the ragged top-2048."""
+    stream over `steps` repetitions: the paged-to-ragged indexer key gather,
+    the ragged fp8 MQA logits [8192 x 131072] (causal windows), the ragged
+    top-2048, the MLA key assembly (the cached prefix restored from the paged
+    fp8 MLA cache, then the chunk's fresh bf16 rows) and the sparse MLA
+    prefill over the assembled keys."""
+    import numpy as np
     import torch
 
-    from nanoengine_amd import _lib, ops, synth
+    from nanoengine_amd import _lib, mla_utils, ops, synth
     from nanoengine_amd.indexer import gather_indexer_cache
 
     _lib.load()
@@ -212,6 +291,7 @@ def bench_prefill(args):
     q_codes, q_scale = synth.ue8m0_quant_rows(q)
     w = (torch.randn(QN, 64, generator=dgen, device=dev) * 64 ** -0.5 * 128 ** -0.5 * q_scale).float().contiguous()
     q8 = q_codes.view(torch.float8_e4m3fn)
+    cu_q = torch.tensor([0, QN], dtype=torch.int32, device=dev)
     cu_k = torch.tensor([0, KN], dtype=torch.int32, device=dev)
     ks = torch.zeros(QN, dtype=torch.int32, device=dev)
     ke = (KN - QN + 1 + torch.arange(QN, dtype=torch.int32, device=dev)).contiguous()
@@ -221,9 +301,13 @@ def bench_prefill(args):
     keys, scales = gather_indexer_cache(inp.cache, inp.block_tables, cu_k, page_size=64, head_dim=128, total_k=KN)
     ws = torch.empty(ops.topk_workspace_bytes(QN), dtype=torch.uint8, device=dev)
     kvs = scales.view(torch.float32).reshape(-1)
-    # sparse MLA prefill over the chunk's ragged bf16 keys (cached + fresh), 128 heads
+    # the MLA keys: the cached prefix lives in the paged fp8 MLA cache (same
+    # block table as the indexer pages), the chunk's own keys arrive as bf16
     H = args.heads
-    kv_bf16 = torch.randn(KN, 576, generator=dgen, device=dev).to(torch.bfloat16)
+    num_blocks = int(inp.block_tables.max().item()) + 1
+    kv_cache = synth.make_mla_cache(num_blocks, seed=args.seed, device=dev)
+    fresh = torch.randn(QN, 576, generator=dgen, device=dev).to(torch.bfloat16)
+    kv_bf16 = torch.empty(KN, 576, dtype=torch.bfloat16, device=dev)
     q_mla = torch.randn(QN, H, 576, generator=dgen, device=dev).to(torch.bfloat16)
     mla_out = torch.empty(QN, H, 512, dtype=torch.bfloat16, device=dev)
     mla_max = torch.empty(QN, H, dtype=torch.float32, device=dev)
@@ -234,14 +318,23 @@ def bench_prefill(args):
                                                                   scales)),
         ("mqa_logits", lambda: ops.mqa_logits(q8, keys.view(torch.float8_e4m3fn), kvs, w, ks, ke, logits, False)),
         ("topk_transform_ragged", lambda: ops.topk_transform_ragged(logits, lens, ks, ks, idx, K, workspace=ws)),
+        ("mla_prefill_kv", lambda: ops.mla_prefill_kv(kv_cache, inp.block_tables, cu_q, cu_k, fresh, KN, kv_bf16)),
         ("sparse_mla_prefill", lambda: ops.sparse_mla_prefill(q_mla, kv_bf16, idx, scale, out=mla_out,
                                                               max_logits=mla_max, lse=mla_lse)),
     ]
+    only = {"logits": "mqa_logits", "mla": "sparse_mla_prefill", "kv": "mla_prefill_kv"}.get(args.only)
     for _ in range(max(1, args.warmup)):
         for _, fn in stages:
             fn()
     torch.cuda.synchronize()
     steps = max(1, args.steps)
+    if only is not None:
+        # profiling aid: the inputs are built, then only the named stage repeats
+        fn = dict(stages)[only]
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return
     t0 = time.perf_counter()
     for _ in range(steps):
         for _, fn in stages:
@@ -271,20 +364,47 @@ def bench_prefill(args):
                                       "bf16_mfma_frac": round(mla_flops / (mu * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
                                       "heads": H})
     out["topk_transform_ragged"]["GBps"] = round(QN * KN * 4 / (out["topk_transform_ragged"]["us"] * 1e-6) / 1e9, 1)
+    cached = KN - QN
+    kv_bytes = cached * 656 + QN * 576 * 2 + KN * 576 * 2
+    out["mla_prefill_kv"].update({"bytes": kv_bytes, "GBps": round(kv_bytes / (out["mla_prefill_kv"]["us"] * 1e-6)
+                                                                   / 1e9, 1)})
     mq = out["mqa_logits"]
-    print(json.dumps({
+
+    base, parity = None, None
+    if not args.no_cpu_baseline:
+        rows = np.linspace(0, QN - 1, 8).round().astype(np.int64)
+        rt = torch.as_tensor(rows, device=dev)
+        bt_np = inp.block_tables.cpu().numpy()
+        host = {"QN": QN, "KN": KN, "idx_cache": inp.cache.cpu().numpy(), "bt": bt_np,
+                "cu_q": np.array([0, QN]), "cu_k": np.array([0, KN]),
+                "mla_rows": kv_cache.contiguous().reshape(-1, 656).cpu().numpy(),
+                "fresh": fresh.float().cpu().numpy(), "q8": q_codes[rt].cpu().numpy(), "w": w[rt].cpu().numpy(),
+                "q_mla": q_mla[rt].float().cpu().numpy()}
+        used = torch.unique(idx[rt][idx[rt] >= 0])
+        gpu = {"logits": logits[rt].cpu().numpy(), "idx": idx[rt].cpu().numpy(),
+               "kv_rows": kv_bf16[used].float().cpu().numpy(), "o": mla_out[rt].float().cpu().numpy(),
+               "lse": mla_lse[rt].cpu().numpy()}
+        base, parity = cpu_baseline_prefill(host, rows, scale, K, gpu)
+    line = {
         "metric": METRIC, "value": round(QN / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8+bf16", "data": "synthetic",
-        "config": {"workload": "BASELINE config 4: chunked prefill (gather + ragged fp8 MQA logits + ragged "
-                               "top-2048 + sparse MLA prefill over bf16 rows), one layer", "queries": QN,
+        "config": {"workload": "BASELINE config 4: chunked prefill (indexer key gather + ragged fp8 MQA logits + "
+                               "ragged top-2048 + MLA key assembly from the fp8 cache + sparse MLA prefill), "
+                               "one layer", "queries": QN,
                    "keys": KN, "cached_prefix": KN - QN, "index_topk": K, "indexer_heads": 64,
                    "indexer_head_dim": 128, "mla_heads": H, "mla_dims": "576/512", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": mq["TFLOPs"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": mq["fp8_mfma_frac"], "traffic": None, "kernel": "mqa_logits_kernel",
                      "flops_per_launch": flops, "avg_launch_us": mq["us"]},
-        "stages": out, "cpu_baseline": None,
-    }), flush=True)
+        "stages": out, "cpu_baseline": base,
+    }
+    if parity is not None:
+        line["parity"] = parity
+    print(json.dumps(line), flush=True)
+    if parity is not None and not parity["ok"]:
+        print(f"parity FAILED: {parity}", file=sys.stderr)
+        sys.exit(1)
 
 
 def bench_mla_decode(args):

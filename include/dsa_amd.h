@@ -364,6 +364,29 @@ DSA_API int dsa_prefill_windows(const void* cu_seqlens_q, const void* cu_seqlens
                                 int32_t* ke, int64_t* status, void* stream);
 
 
+/* The sparse prefill's ragged bf16 keys [total_k, 576] from the paged fp8
+ * MLA cache (656-byte rows) and the chunk's fresh rows.
+ *   kv_cache   [blocks, block_size, 656] bytes, block stride kv_block_stride_bytes
+ *   block_table [num_seqs, M] int32 (row stride bt_stride)
+ *   cu_seqlens_q/_k [num_seqs + 1] int32 (cu_is_64 = 0) or int64; sequence b's
+ *              fresh queries are the last q_len of its k_len keys
+ *   fresh      [cu_q[-1], 576] bf16 rows (row stride fresh_row_stride elements)
+ *   out        [total_k = cu_k[-1], 576] bf16 (row stride out_row_stride)
+ * Key i of sequence b is its cached row i, dequantised (nope = e4m3 x tile
+ * scale, exact in bf16; rope copied), while i < k_len - q_len, else fresh row
+ * cu_q[b] + i - (k_len - q_len).
+ * Replaces _gather_cache_cached_only + restore_mla_fp8_cache_rows +
+ * _interleave_cached_fresh (dlengine/runtime/layers/backends/attention/
+ * mla_utils.py:118-236, kernel/triton/hopper/fp8_utils.py:153-196) as called at
+ * dlengine/runtime/models/deepseek_v2/deepseek_v2.py:1573-1604. */
+DSA_API int dsa_mla_prefill_kv(const uint8_t* kv_cache, int64_t kv_block_stride_bytes,
+                               int kv_block_size, const int32_t* block_table, int64_t bt_stride,
+                               const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64,
+                               int num_seqs, int64_t total_k, const void* fresh,
+                               int64_t fresh_row_stride, void* out, int64_t out_row_stride,
+                               void* stream);
+
+
 /* Sparse MLA prefill over ragged bf16 KV rows.
  *   q          [num_tokens, num_heads, 576] bf16 (row stride q_token_stride, head
  *              stride q_head_stride elements, last dim contiguous)

@@ -104,6 +104,57 @@ gather_indexer_cache_kernel(const uint8_t* __restrict__ cache, int64_t page_byte
         *reinterpret_cast<const uint32_t*>(base + (int64_t)page_size * 128 + off * 4);
 }
 
+
+// The sparse prefill's keys in ragged order, from the paged fp8 MLA cache and
+// the chunk's fresh bf16 rows, in one pass: the gather of the cached prefix
+// (dlengine/runtime/layers/backends/attention/mla_utils.py:200-234), its
+// restore to bf16 (kernel/triton/hopper/fp8_utils.py:153-196) and the
+// cached/fresh interleave (mla_utils.py:118-165) as the prefill calls them at
+// dlengine/runtime/models/deepseek_v2/deepseek_v2.py:1573-1604.
+// Key row r of sequence b (cu_k[b] <= r < cu_k[b+1]) at i = r - cu_k[b] is
+// cached row i of the sequence when i < k_len - q_len (read through
+// block_table[b]), else fresh row cu_q[b] + i - (k_len - q_len). One wave per
+// row: for a cached row lane l dequantises nope bytes 8l .. 8l+7 with the
+// scale of tile l/16 (exact: fp8 times a power of two is a bf16 value) and
+// writes 16 bytes; lanes 0-7 copy the 128-byte bf16 rope tail. A fresh row is
+// a 1152-byte copy in 16-byte pieces.
+__global__ void __launch_bounds__(256)
+mla_prefill_kv_kernel(const uint8_t* __restrict__ cache, int64_t block_stride, int block_size,
+                      const int32_t* __restrict__ block_table, int64_t bt_stride, const void* __restrict__ cu_q,
+                      const void* __restrict__ cu_k, int cu_is_64, int num_seqs, int64_t total_k,
+                      const uint16_t* __restrict__ fresh, int64_t fresh_stride, uint16_t* __restrict__ out,
+                      int64_t out_stride) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= total_k) return;
+  int lo = 0, hi = num_seqs;  // largest b < num_seqs with cu_k[b] <= r
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (load_slot(cu_k, cu_is_64, mid) <= r) lo = mid; else hi = mid;
+  }
+  const int64_t k0 = load_slot(cu_k, cu_is_64, lo), k1 = load_slot(cu_k, cu_is_64, lo + 1);
+  const int64_t q0 = load_slot(cu_q, cu_is_64, lo), q1 = load_slot(cu_q, cu_is_64, lo + 1);
+  const int64_t i = r - k0, cached = (k1 - k0) - (q1 - q0);
+  uint8_t* dst = reinterpret_cast<uint8_t*>(out + r * out_stride);
+  if (i < cached) {
+    const int64_t blk = block_table[(int64_t)lo * bt_stride + i / block_size];
+    const uint8_t* row = cache + blk * block_stride + (i % block_size) * 656;
+    const uint2 codes = *reinterpret_cast<const uint2*>(row + 8 * lane);
+    const float scale = reinterpret_cast<const float*>(row + 512)[lane >> 4];
+    v4i o;
+    o[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, false));
+    o[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, true));
+    o[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, false));
+    o[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, true));
+    *reinterpret_cast<v4i*>(dst + 16 * lane) = o;
+    if (lane < 8) *reinterpret_cast<v4i*>(dst + 1024 + 16 * lane) = *reinterpret_cast<const v4i*>(row + 528 + 16 * lane);
+  } else {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(fresh + (q0 + i - cached) * fresh_stride);
+    *reinterpret_cast<v4i*>(dst + 16 * lane) = *reinterpret_cast<const v4i*>(src + 16 * lane);
+    if (lane < 8) *reinterpret_cast<v4i*>(dst + 1024 + 16 * lane) = *reinterpret_cast<const v4i*>(src + 1024 + 16 * lane);
+  }
+}
+
 }  // namespace dsa
 
 extern "C" {
@@ -158,6 +209,30 @@ int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, int page_
                      page_bytes, page_size, block_table, bt_stride, cu_seqlens_k, cu_is_64, num_seqs, total_k,
                      key_out, scale_out);
   return check_launch("dsa_gather_indexer_cache");
+}
+
+int dsa_mla_prefill_kv(const uint8_t* kv_cache, int64_t kv_block_stride_bytes, int kv_block_size,
+                       const int32_t* block_table, int64_t bt_stride, const void* cu_seqlens_q,
+                       const void* cu_seqlens_k, int cu_is_64, int num_seqs, int64_t total_k, const void* fresh,
+                       int64_t fresh_row_stride, void* out, int64_t out_row_stride, void* stream) {
+  using namespace dsa;
+  if (num_seqs < 1 || total_k < 0 || kv_block_size <= 0 || fresh_row_stride < 576 || out_row_stride < 576 ||
+      kv_block_stride_bytes < (int64_t)kv_block_size * 656)
+    return set_error(kInvalidArgument, "dsa_mla_prefill_kv: bad sizes");
+  if (total_k == 0) return kOk;
+  if (!kv_cache || !block_table || !cu_seqlens_q || !cu_seqlens_k || !fresh || !out)
+    return set_error(kInvalidArgument, "dsa_mla_prefill_kv: null pointer");
+  if (((reinterpret_cast<uintptr_t>(kv_cache) | reinterpret_cast<uintptr_t>(fresh) |
+        reinterpret_cast<uintptr_t>(out)) & 15) || (kv_block_stride_bytes & 15) || (fresh_row_stride & 7) ||
+      (out_row_stride & 7))
+    return set_error(kInvalidArgument, "dsa_mla_prefill_kv: cache, fresh rows and output rows must be 16-byte aligned");
+  const int64_t nwg = (total_k + 3) / 4;
+  if (nwg > INT32_MAX) return set_error(kInvalidArgument, "dsa_mla_prefill_kv: too many rows");
+  hipLaunchKernelGGL(mla_prefill_kv_kernel, dim3((unsigned)nwg), dim3(256), 0, (hipStream_t)stream, kv_cache,
+                     kv_block_stride_bytes, kv_block_size, block_table, bt_stride, cu_seqlens_q, cu_seqlens_k,
+                     cu_is_64, num_seqs, total_k, static_cast<const uint16_t*>(fresh), fresh_row_stride,
+                     static_cast<uint16_t*>(out), out_row_stride);
+  return check_launch("dsa_mla_prefill_kv");
 }
 
 }  // extern "C"

@@ -487,6 +487,29 @@ def mqa_logits(q_fp8: torch.Tensor, kv_fp8: torch.Tensor, kv_scale: torch.Tensor
               out.data_ptr(), out.stride(0), out.shape[1], int(bool(clean_logits)), _stream(dev))
 
 
+def mla_prefill_kv(k_cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                   cu_seqlens_k: torch.Tensor, fresh: torch.Tensor, total_k: int, out: torch.Tensor) -> None:
+    """Ragged bf16 keys [total_k, 576] of a prefill chunk: cached rows restored
+    from the fp8 cache, fresh rows copied (see dsa_mla_prefill_kv)."""
+    blk_stride, block_size = mla_kv_geometry(k_cache)
+    _require(cu_seqlens_q.dtype == cu_seqlens_k.dtype and cu_seqlens_q.dtype in (torch.int32, torch.int64),
+             "cu_seqlens_q/_k must share one dtype, int32 or int64", ValueError)
+    _require(cu_seqlens_q.dim() == 1 and cu_seqlens_q.shape == cu_seqlens_k.shape and cu_seqlens_q.is_contiguous()
+             and cu_seqlens_k.is_contiguous(), "cu_seqlens_q/_k must be contiguous [num_seqs + 1]", ValueError)
+    num_seqs = cu_seqlens_q.numel() - 1
+    _require(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == num_seqs
+             and block_table.stride(1) == 1, "block_table must be int32 [num_seqs, M]", ValueError)
+    _require(fresh.dtype == torch.bfloat16 and fresh.dim() == 2 and fresh.shape[1] == MLA_D_QK
+             and fresh.stride(1) == 1, f"fresh must be bf16 [q, {MLA_D_QK}]", ValueError)
+    _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (total_k, MLA_D_QK) and out.stride(1) == 1,
+             f"out must be bf16 [{total_k}, {MLA_D_QK}]", ValueError)
+    dev = _check_cuda(k_cache, block_table, cu_seqlens_q, cu_seqlens_k, fresh, out)
+    _lib.call("dsa_mla_prefill_kv", _as_bytes(k_cache).data_ptr(), blk_stride, block_size, block_table.data_ptr(),
+              block_table.stride(0), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+              int(cu_seqlens_q.dtype == torch.int64), num_seqs, int(total_k), fresh.data_ptr(), fresh.stride(0),
+              out.data_ptr(), out.stride(0), _stream(dev))
+
+
 def prefill_windows(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, num_queries: int, page_size: int,
                     ks: torch.Tensor, ke: torch.Tensor, status: torch.Tensor) -> None:
     """Per-query key windows [ks, ke) of a ragged prefill batch and the batch's

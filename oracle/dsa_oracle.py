@@ -19,7 +19,7 @@ from __future__ import annotations
 import numpy as np
 
 __all__ = [
-    "FP8_MAX", "D_NOPE", "D_ROPE", "D_QK", "MLA_ROW_BYTES", "MLA_TILE",
+    "FP8_MAX", "assemble_prefill_kv", "D_NOPE", "D_ROPE", "D_QK", "MLA_ROW_BYTES", "MLA_TILE",
     "fp8_e4m3fn_decode", "fp8_e4m3fn_encode", "bf16_to_f32", "f32_to_bf16",
     "ue8m0_ceil", "quantize_rows_ue8m0", "pack_indexer_cache", "indexer_cache_token",
     "quantize_mla_rows", "unpack_mla_rows", "dequant_mla_rows",
@@ -109,6 +109,30 @@ def ue8m0_ceil(scale: np.ndarray) -> np.ndarray:
     m, e = np.frexp(s.astype(np.float64))          # s = m * 2^e, m in [0.5, 1)
     k = np.where(m == 0.5, e - 1, e)               # exact power of two: 2^(e-1)
     return np.ldexp(np.float64(1.0), k).astype(np.float32)
+
+
+def assemble_prefill_kv(cache_rows: np.ndarray, block_size: int, block_table: np.ndarray,
+                        cu_seqlens_q: np.ndarray, cu_seqlens_k: np.ndarray, fresh: np.ndarray) -> np.ndarray:
+    """The sparse prefill's ragged keys [total_k, 576] float32 (bf16 values).
+
+    Restates deepseek_v2.py:1573-1604: ``_gather_cache_cached_only``
+    (mla_utils.py:200-234: the first ``k_len - q_len`` tokens of each sequence,
+    through its block table), ``restore_mla_fp8_cache_rows`` (fp8_utils.py:
+    180-196, the 656-byte layout -> ``dequant_mla_rows``) and
+    ``_interleave_cached_fresh`` (mla_utils.py:118-165: per sequence the cached
+    rows, then the fresh ones). ``cache_rows`` is the cache as [blocks *
+    block_size, 656] bytes; ``fresh`` [total_q, 576] holds bf16 values."""
+    cq = np.asarray(cu_seqlens_q, dtype=np.int64)
+    ck = np.asarray(cu_seqlens_k, dtype=np.int64)
+    parts = []
+    for b in range(len(cq) - 1):
+        q_len, k_len = cq[b + 1] - cq[b], ck[b + 1] - ck[b]
+        cached = k_len - q_len
+        slots = [int(block_table[b, i // block_size]) * block_size + i % block_size for i in range(cached)]
+        if cached:
+            parts.append(dequant_mla_rows(cache_rows[np.asarray(slots)]))
+        parts.append(np.asarray(fresh[cq[b]:cq[b + 1]], dtype=np.float32))
+    return np.concatenate(parts) if parts else np.zeros((0, D_QK), np.float32)
 
 
 # --------------------------------------------------------------------------- indexer formats

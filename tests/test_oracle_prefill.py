@@ -97,3 +97,23 @@ def test_mqa_logits_equals_paged_decode_logits():
     assert np.array_equal(g_keys, keys) and np.array_equal(g_scales, scales)
     pre = O.mqa_logits(q[0], g_keys, g_scales, w, np.array([0]), np.array([L]))
     np.testing.assert_allclose(pre, dec, rtol=1e-6)
+
+
+def test_assemble_prefill_kv_known_answer():
+    """Two sequences over a 2-row-block cache: sequence 0 has 2 cached keys
+    (slots 2, 3 through block_table [1, 0]) and 1 fresh; sequence 1 is all
+    fresh. Row values are small integers, exact through fp8 and bf16."""
+    slots = 4
+    src = np.zeros((slots, 576), np.float32)
+    for s in range(slots):
+        src[s, :512] = s + 1
+        src[s, 512:] = -(s + 1)
+    cache = O.quantize_mla_rows(src)
+    fresh = np.stack([np.full(576, 100.0 + j, np.float32) for j in range(3)])
+    got = O.assemble_prefill_kv(cache, 2, np.array([[1, 0], [0, 1]]), np.array([0, 1, 3]), np.array([0, 3, 5]),
+                                fresh)
+    exp = np.stack([src[2], src[3], fresh[0], fresh[1], fresh[2]])
+    assert np.array_equal(got, exp)
+    # no cached prefix anywhere: the fresh rows unchanged
+    assert np.array_equal(O.assemble_prefill_kv(cache, 2, np.zeros((1, 1), int), np.array([0, 3]),
+                                                np.array([0, 3]), fresh), fresh)
