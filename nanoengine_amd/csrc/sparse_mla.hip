@@ -22,13 +22,14 @@
 //            a table read and an add. Invalid indices read a zero row.
 //   QK     : wave (kh = q/2, d = q%2) forms the partial S^T[32 keys x 32
 //            heads] of keys 32kh..32kh+31 over nope dims [256d, 256d+256)
-//            and rope dims [32d, 32d+32). The nope part runs on
-//            v_mfma_scale_f32_32x32x64_f8f6f4: A = the raw fp8 rows from LDS
-//            with the row's tile scale as the E8M0 block scale (the cache's
-//            scales are powers of two, so this is exact); B = the query as two
-//            fp8 terms hi + lo with per-chunk E8M0 scales, which together hold
-//            each bf16 query value to ~2^-22 of its chunk's largest. The rope
-//            part (bf16 in the row) runs on v_mfma_f32_32x32x16_bf16.
+//            and rope dims [32d, 32d+32), all on v_mfma_f32_32x32x16_bf16:
+//            A = the key's fp8 nope bytes from LDS converted to bf16 with the
+//            row's tile scale (v_cvt_scalef32_pk_bf16_fp8; exact, since an
+//            e4m3 value times a power of two is a bf16 value) and its bf16
+//            rope; B = the query's bf16 values as given. Products are exact
+//            and sums are f32, as in a bf16 dequantise-then-multiply. (The
+//            scaled fp8 MFMA would take the raw rows directly, but it sums its
+//            64 products to only ~14 bits below the largest one.)
 //   reduce : the two dim halves are summed by a reduce-scatter through LDS:
 //            wave (kh, d) ends with the full scores of keys 16o..16o+15,
 //            o = 2kh + d, so each score is exponentiated exactly once.
@@ -162,21 +163,6 @@ __device__ __forceinline__ v8bf fp8x8_to_bf16(v2i raw) {
   return as_v8bf(r);
 }
 
-// E8M0 exponent (biased) of 2^(ceil(log2 v) - 8) for v >= 0: v * 2^-e stays
-// within +-256, inside the e4m3 range. Exact bit arithmetic; v = 0 gives 2^0.
-__device__ __forceinline__ int e8m0_for(float v) {
-  const uint32_t u = __float_as_uint(v);
-  if (u == 0u) return 127;
-  int e = (int)((u >> 23) & 0xffu);
-  const uint32_t m = u & 0x7fffffu;
-  int cl;  // ceil(log2 v)
-  if (e == 0) cl = (32 - __clz(m)) - 149 - ((m & (m - 1)) ? 0 : 1);
-  else cl = e - 127 + (m ? 1 : 0);
-  return min(max(cl - 8 + 127, 1), 254);
-}
-__device__ __forceinline__ float e8m0_value(int e) { return __uint_as_float((uint32_t)e << 23); }
-__device__ __forceinline__ float e8m0_inv(int e) { return __uint_as_float((uint32_t)(254 - e) << 23); }
-
 __device__ __forceinline__ v8i lds_read32(const uint8_t* p) {
   const v4i a = *reinterpret_cast<const v4i*>(p);
   const v4i b = *reinterpret_cast<const v4i*>(p + 16);
@@ -184,24 +170,6 @@ __device__ __forceinline__ v8i lds_read32(const uint8_t* p) {
   r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
   r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
   return r;
-}
-
-// D = A . B + C on v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 x e4m3), with the
-// E8M0 scales taken from byte `sa_byte` of sa and byte `sb_byte` of sb. A lane
-// (row i, half h) holds k = 16h + 0..15 in bytes 0-15 and k = 32 + 16h + 0..15 in
-// bytes 16-31; the scale of k-block b of row i is read from lane 32b + i.
-template <int kSaByte, int kSbByte>
-__device__ __forceinline__ v16f mfma_fp8_32(v8i a, v8i b, v16f c, int sa, int sb) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, kSaByte, sa, kSbByte, sb);
-}
-// chunk c of a wave's 256 nope dims: row-scale byte c/2 (tile 2d + c/2), query-scale byte c
-__device__ __forceinline__ v16f mfma_fp8_chunk(int c, v8i a, v8i b, v16f acc, int sa, int sb) {
-  switch (c) {
-    case 0: return mfma_fp8_32<0, 0>(a, b, acc, sa, sb);
-    case 1: return mfma_fp8_32<0, 1>(a, b, acc, sa, sb);
-    case 2: return mfma_fp8_32<1, 2>(a, b, acc, sa, sb);
-    default: return mfma_fp8_32<1, 3>(a, b, acc, sa, sb);
-  }
 }
 
 // The gather of one block. One wave writes the 64 row addresses of the block
@@ -339,60 +307,20 @@ sparse_mla_kernel(const MlaParams P) {
   if (wave == kIdxWave)
     for (int j = 0; j < 4 && j < nblk; ++j) issue_index(P, smem, t, key_begin, j, lane);
 
-  // Query B operands. Nope chunk c (dims 256d + 64c + 32h + 0..31 for lane half
-  // h) as two fp8 terms q = 2^e_hi * hi + 2^e_lo * lo with one E8M0 exponent per
-  // (head, 64-dim chunk): hi takes the top 4 significant bits of each bf16
-  // value and lo the rest, so the pair holds q to ~2^-22 of the chunk's
-  // largest value (bf16 has 8 significant bits; e4m3 normals span 2^15).
-  // Rope k-step rho: bf16 dims 32d + 16rho + 8h + 0..7.
-  v8i qhi[4], qlo[4];
-  int qe_hi = 0, qe_lo = 0;  // byte c: biased exponent of chunk c
+  // Query B operands, bf16 as given: nope chunk c (64 dims), k-step j holds
+  // dims 256d + 64c + 32h + 8j .. +7 for lane half h, the same dims the key
+  // operand converts from its row bytes. Rope k-step rho: bf16 dims
+  // 32d + 16rho + 8h + 0..7.
+  v4i qn[4][4];
   v4i qr[2];
   {
     const uint16_t* qh = P.q + (int64_t)t * P.q_tok_stride + (int64_t)(head_ok ? head : 0) * P.q_head_stride;
     const v4i z = {0, 0, 0, 0};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint16_t* p = qh + 256 * d + 64 * c + 32 * h;
-      float x[32];
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const v4i w = head_ok ? *reinterpret_cast<const v4i*>(p + 8 * i) : z;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[8 * i + 2 * e] = __uint_as_float((uint32_t)w[e] << 16);
-          x[8 * i + 2 * e + 1] = __uint_as_float((uint32_t)w[e] & 0xffff0000u);
-        }
-      }
-      float amax = 0.f;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
-      amax = fmaxf(amax, shfl_xor(amax, 32));
-      const int ehi = e8m0_for(amax);
-      const float inv_hi = e8m0_inv(ehi);
-      const float s_hi = e8m0_value(ehi);
-      float r[32];
-      float rmax = 0.f;
-#pragma unroll
-      for (int i = 0; i < 32; i += 4) {
-        const uint32_t w = f32x4_to_fp8(x[i] * inv_hi, x[i + 1] * inv_hi, x[i + 2] * inv_hi, x[i + 3] * inv_hi);
-        qhi[c][i / 4] = (int)w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const v2f dq = fp8x2_to_f32(w >> (16 * (e >> 1)), false);
-          r[i + e] = x[i + e] - dq[e & 1] * s_hi;  // exact
-          rmax = fmaxf(rmax, fabsf(r[i + e]));
-        }
-      }
-      rmax = fmaxf(rmax, shfl_xor(rmax, 32));
-      const int elo = e8m0_for(rmax);
-      const float inv_lo = e8m0_inv(elo);
-#pragma unroll
-      for (int i = 0; i < 32; i += 4)
-        qlo[c][i / 4] = (int)f32x4_to_fp8(r[i] * inv_lo, r[i + 1] * inv_lo, r[i + 2] * inv_lo, r[i + 3] * inv_lo);
-      qe_hi |= ehi << (8 * c);
-      qe_lo |= elo << (8 * c);
-    }
+      for (int j = 0; j < 4; ++j)
+        qn[c][j] = head_ok ? *reinterpret_cast<const v4i*>(qh + 256 * d + 64 * c + 32 * h + 8 * j) : z;
 #pragma unroll
     for (int rho = 0; rho < 2; ++rho)
       qr[rho] = head_ok ? *reinterpret_cast<const v4i*>(qh + 512 + 32 * d + 16 * rho + 8 * h) : z;
@@ -466,17 +394,26 @@ sparse_mla_kernel(const MlaParams P) {
     {
       const uint8_t* row = buf + (32 * kh + c32) * kMlaRowBytes;
       const v2f ksc = *reinterpret_cast<const v2f*>(row + 512 + 8 * d);
-      // E8M0 of the row's tile scales (powers of two): byte tt = tile 2d + tt
-      const int ke = (int)(((__float_as_uint(ksc[0]) >> 23) & 0xffu) | (((__float_as_uint(ksc[1]) >> 23) & 0xffu) << 8));
-      // K chunk c: lane half h holds bytes 256d + 64c + 32h .. +32 of key 32kh + c32
+      // K chunk c: lane half h holds bytes 256d + 64c + 32h .. +32 of key
+      // 32kh + c32, dequantised to bf16 with the tile scale (exact: an e4m3
+      // value times a power of two is a bf16 value), 8 per k-step
       const uint8_t* krow = row + 256 * d + 32 * h;
       v8i kraw[2];
       kraw[0] = lds_read32(krow);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         if (c + 1 < 4) kraw[(c + 1) & 1] = lds_read32(krow + 64 * (c + 1));
-        s = mfma_fp8_chunk(c, kraw[c & 1], qhi[c], s, ke, qe_hi);
-        s = mfma_fp8_chunk(c, kraw[c & 1], qlo[c], s, ke, qe_lo);
+        const float sc = ksc[c >> 1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v8i& kr = kraw[c & 1];
+          v4i kb;
+          kb[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j], sc, false));
+          kb[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j], sc, true));
+          kb[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j + 1], sc, false));
+          kb[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j + 1], sc, true));
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(kb), as_v8bf(qn[c][j]), s, 0, 0, 0);
+        }
       }
 #pragma unroll
       for (int rho = 0; rho < 2; ++rho) {

@@ -2,9 +2,9 @@
 
 Tolerances (north star): o within bf16 atol 2e-2, LSE within 1e-3 (absolute,
 natural log). The rows' fp8 values times their power-of-two tile scales are
-exact in the MFMA inputs; the query enters the fp8 score MFMA as two fp8 terms
-that hold it to ~2^-22 of each 64-dim chunk's largest value. The remaining
-differences are the bf16 rounding of P and the fp32 accumulation order.
+exact in bf16, so the score products are exact and only their f32 summation
+rounds. The remaining differences are the bf16 rounding of P and the fp32
+accumulation order.
 """
 import numpy as np
 import pytest
@@ -204,3 +204,55 @@ def test_schedule_keeps_workspaces_for_captured_graphs(cuda):
             for a, b in zip(outs, eager):
                 assert torch.equal(a, b), T
     del junk
+
+
+def _query_error_bound_case(seed):
+    """Queries whose 64-dim nope chunks each span ~24 binades (one anchor value
+    and the rest spread down to 2^-24 of it, random signs), one valid key per
+    query, so LSE = sm_scale * q.k with nothing else in it."""
+    T, H, K = 4, 128, 64
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    mag = torch.exp2(-24 * torch.rand(T, H, 512, generator=g))
+    anchor = torch.exp2(torch.randint(-3, 7, (T, H, 8, 1), generator=g).float())
+    nope = (mag.view(T, H, 8, 64) * anchor).view(T, H, 512)
+    nope[..., ::64] = anchor[..., 0]                      # an exact power of two at each chunk's maximum
+    nope *= torch.where(torch.rand(T, H, 512, generator=g) < 0.5, -1.0, 1.0)
+    rope = torch.randn(T, H, 64, generator=g)
+    q = torch.cat([nope, rope], -1).to(torch.bfloat16)
+    kv = synth.make_mla_cache(4, seed=seed)
+    idx = torch.full((T, K), -1, dtype=torch.int32)
+    idx[:, 0] = torch.randperm(4 * 64, generator=g)[:T].to(torch.int32)
+    return q, kv, idx
+
+
+def test_qk_score_error_bound(cuda):
+    """Bound on the score error of the QK product.
+
+    The key's fp8 codes times their power-of-two tile scale are exact in bf16,
+    the query enters as the caller's bf16, and the bf16 MFMA forms exact
+    products summed in f32, so |s - s_exact| stays within f32 accumulation
+    error: 2^-18 sum_d |q_d k_d| is a safe bound for 576 terms (plus f32
+    rounding of the result). The query chunks span ~24 binades each, so any
+    quantisation of the query to fp8 (one e4m3 term with a per-64-dim scale)
+    breaks the bound by orders of magnitude; the scores are read from the LSE
+    of a single valid key."""
+    print("mla qk score bound", flush=True)
+    q, kv, idx = _query_error_bound_case(seed=41)
+    sm_scale = 1.0
+    o, lse = ops.sparse_mla_decode(q.to(cuda), kv, idx.to(cuda), sm_scale)
+    torch.cuda.synchronize()
+    rows = O.dequant_mla_rows(kv.contiguous().reshape(-1, 656).cpu().numpy()).astype(np.float64)
+    k = rows[idx[:, 0].numpy()]                                         # [T, 576]
+    qf = q.float().numpy().astype(np.float64)                            # [T, H, 576]
+    exact = np.einsum("thd,td->th", qf, k)
+    got = lse.cpu().numpy().astype(np.float64) / sm_scale
+    accum = np.einsum("thd,td->th", np.abs(qf), np.abs(k))
+    bound = 2.0 ** -18 * accum + 2.0 ** -22 * np.abs(exact)
+    err = np.abs(got - exact)
+    assert np.all(err <= bound), f"worst err/bound {np.max(err / bound):.3g}"
+    # the data defeats an fp8 query: one e4m3 term per value, scale 2^(ceil(log2 amax) - 8) per chunk
+    x = qf[..., :512].reshape(*qf.shape[:2], 8, 64)
+    s_hi = np.exp2(np.ceil(np.log2(np.abs(x).max(-1))) - 8)[..., None]
+    hi = O.fp8_e4m3fn_decode(O.fp8_e4m3fn_encode(x / s_hi)) * s_hi
+    err_hi = np.abs(np.einsum("thcd,tcd->th", hi - x, k[:, :512].reshape(-1, 8, 64)))
+    assert np.median(err_hi / bound) > 100
