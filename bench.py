@@ -273,9 +273,10 @@ def bench_prefill(args):
     (131072 keys in all). Stages, each timed with HIP events on the launch
     stream over `steps` repetitions: the paged-to-ragged indexer key gather,
     the ragged fp8 MQA logits [8192 x 131072] (causal windows), the ragged
-    top-2048, the MLA key assembly (the cached prefix restored from the paged
-    fp8 MLA cache, then the chunk's fresh bf16 rows) and the sparse MLA
-    prefill over the assembled keys."""
+    top-2048 and the sparse MLA prefill: the selected keys of the cached prefix
+    read from the paged fp8 MLA cache, those of the chunk's fresh keys as bf16
+    rows (dsa_sparse_mla_prefill_paged). The reference's route (the keys
+    assembled as bf16 rows, then the bf16 sparse prefill) is timed beside it."""
     import numpy as np
     import torch
 
@@ -313,24 +314,38 @@ def bench_prefill(args):
     mla_max = torch.empty(QN, H, dtype=torch.float32, device=dev)
     mla_lse = torch.empty(QN, H, dtype=torch.float32, device=dev)
     scale = 192 ** -0.5
+    pws = torch.empty(ops.sparse_mla_prefill_paged_workspace_bytes(QN, K), dtype=torch.uint8, device=dev)
     stages = [
         ("gather_indexer_cache", lambda: ops.gather_indexer_cache(inp.cache, inp.block_tables, cu_k, 64, KN, keys,
                                                                   scales)),
         ("mqa_logits", lambda: ops.mqa_logits(q8, keys.view(torch.float8_e4m3fn), kvs, w, ks, ke, logits, False)),
         ("topk_transform_ragged", lambda: ops.topk_transform_ragged(logits, lens, ks, ks, idx, K, workspace=ws)),
-        ("mla_prefill_kv", lambda: ops.mla_prefill_kv(kv_cache, inp.block_tables, cu_q, cu_k, fresh, KN, kv_bf16)),
-        ("sparse_mla_prefill", lambda: ops.sparse_mla_prefill(q_mla, kv_bf16, idx, scale, out=mla_out,
-                                                              max_logits=mla_max, lse=mla_lse)),
+        # the cached keys straight from the paged fp8 cache, the fresh keys as bf16 rows
+        ("sparse_mla_prefill_paged", lambda: ops.sparse_mla_prefill_paged(
+            q_mla, kv_cache, inp.block_tables, cu_q, cu_k, fresh, idx, scale, KN, out=mla_out, max_logits=mla_max,
+            lse=mla_lse, workspace=pws)),
     ]
-    only = {"logits": "mqa_logits", "mla": "sparse_mla_prefill", "kv": "mla_prefill_kv"}.get(args.only)
+    # the same attention through the assembled bf16 keys, timed beside the step
+    alt_out = torch.empty_like(mla_out)
+    alt_max, alt_lse = torch.empty_like(mla_max), torch.empty_like(mla_lse)
+    alternative = [
+        ("mla_prefill_kv", lambda: ops.mla_prefill_kv(kv_cache, inp.block_tables, cu_q, cu_k, fresh, KN, kv_bf16)),
+        ("sparse_mla_prefill", lambda: ops.sparse_mla_prefill(q_mla, kv_bf16, idx, scale, out=alt_out,
+                                                              max_logits=alt_max, lse=alt_lse)),
+    ]
+    only = {"logits": "mqa_logits", "mla": "sparse_mla_prefill_paged", "kv": "mla_prefill_kv",
+            "mlabf16": "sparse_mla_prefill"}.get(args.only)
     for _ in range(max(1, args.warmup)):
         for _, fn in stages:
             fn()
     torch.cuda.synchronize()
     steps = max(1, args.steps)
+    for _, fn in alternative:
+        fn()
+    torch.cuda.synchronize()
     if only is not None:
         # profiling aid: the inputs are built, then only the named stage repeats
-        fn = dict(stages)[only]
+        fn = dict(stages + alternative)[only]
         for _ in range(steps):
             fn()
         torch.cuda.synchronize()
@@ -342,7 +357,7 @@ def bench_prefill(args):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     out = {}
-    for name, fn in stages:
+    for name, fn in stages + alternative:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
@@ -359,15 +374,17 @@ def bench_prefill(args):
                               "logits_bytes": QN * KN * 4})
     mla_pairs = int((idx >= 0).sum().item())
     mla_flops = 2.0 * H * (576 + 512) * mla_pairs
-    mu = out["sparse_mla_prefill"]["us"]
-    out["sparse_mla_prefill"].update({"flops": mla_flops, "TFLOPs": round(mla_flops / (mu * 1e-6) / 1e12, 1),
-                                      "bf16_mfma_frac": round(mla_flops / (mu * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                                      "heads": H})
+    fresh_pairs = int((idx >= KN - QN).sum().item())
+    for name in ("sparse_mla_prefill_paged", "sparse_mla_prefill"):
+        mu = out[name]["us"]
+        out[name].update({"flops": mla_flops, "TFLOPs": round(mla_flops / (mu * 1e-6) / 1e12, 1),
+                          "bf16_mfma_frac": round(mla_flops / (mu * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                          "heads": H})
+    out["sparse_mla_prefill_paged"]["fresh_key_share"] = round(fresh_pairs / max(mla_pairs, 1), 4)
+    out["alternative_assembled_bf16"] = {"us": round(out.pop("mla_prefill_kv")["us"] + out["sparse_mla_prefill"]["us"], 1),
+                                         "stages": ["mla_prefill_kv", "sparse_mla_prefill"],
+                                         "sparse_mla_prefill": out.pop("sparse_mla_prefill")}
     out["topk_transform_ragged"]["GBps"] = round(QN * KN * 4 / (out["topk_transform_ragged"]["us"] * 1e-6) / 1e9, 1)
-    cached = KN - QN
-    kv_bytes = cached * 656 + QN * 576 * 2 + KN * 576 * 2
-    out["mla_prefill_kv"].update({"bytes": kv_bytes, "GBps": round(kv_bytes / (out["mla_prefill_kv"]["us"] * 1e-6)
-                                                                   / 1e9, 1)})
     mq = out["mqa_logits"]
 
     base, parity = None, None
@@ -381,6 +398,7 @@ def bench_prefill(args):
                 "fresh": fresh.float().cpu().numpy(), "q8": q_codes[rt].cpu().numpy(), "w": w[rt].cpu().numpy(),
                 "q_mla": q_mla[rt].float().cpu().numpy()}
         used = torch.unique(idx[rt][idx[rt] >= 0])
+        ops.mla_prefill_kv(kv_cache, inp.block_tables, cu_q, cu_k, fresh, KN, kv_bf16)   # rows for the key check
         gpu = {"logits": logits[rt].cpu().numpy(), "idx": idx[rt].cpu().numpy(),
                "kv_rows": kv_bf16[used].float().cpu().numpy(), "o": mla_out[rt].float().cpu().numpy(),
                "lse": mla_lse[rt].cpu().numpy()}
@@ -390,8 +408,8 @@ def bench_prefill(args):
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8+bf16", "data": "synthetic",
         "config": {"workload": "BASELINE config 4: chunked prefill (indexer key gather + ragged fp8 MQA logits + "
-                               "ragged top-2048 + MLA key assembly from the fp8 cache + sparse MLA prefill), "
-                               "one layer", "queries": QN,
+                               "ragged top-2048 + sparse MLA prefill over the paged fp8 cache and the fresh bf16 "
+                               "rows), one layer", "queries": QN,
                    "keys": KN, "cached_prefix": KN - QN, "index_topk": K, "indexer_heads": 64,
                    "indexer_head_dim": 128, "mla_heads": H, "mla_dims": "576/512", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": mq["TFLOPs"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",

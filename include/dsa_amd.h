@@ -346,6 +346,40 @@ DSA_API int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, i
                                      void* stream);
 
 
+/* Sparse MLA prefill straight from the paged fp8 MLA cache: the keys a token
+ * selects from its sequence's cached prefix are read as 656-byte rows through
+ * the block table and dequantised exactly in registers (the decode kernel);
+ * only the keys it selects among the chunk's fresh rows are read as bf16.
+ * The two partial results are merged by LSE.
+ *   q, indices, num_tokens, num_heads, topk, sm_scale, out, max_logits, lse:
+ *              as dsa_sparse_mla_prefill, with indices into the ragged key
+ *              order of total_k = cu_k[-1] keys (sequence b's keys at cu_k[b] ..)
+ *   kv_cache   [blocks, kv_block_size, 656] bytes (block stride, block count)
+ *   block_table [num_seqs, M] int32; cu_seqlens_q/_k [num_seqs + 1] int32
+ *              (cu_is_64 = 0) or int64: key i of sequence b is cached row i
+ *              while i < k_len - q_len, else fresh row cu_q[b] + i - (k_len - q_len)
+ *   fresh      [total_q, 576] bf16 (row stride fresh_row_stride elements)
+ *   workspace  dsa_sparse_mla_prefill_paged_workspace_bytes(num_tokens, topk)
+ * Same result as assembling the keys (dsa_mla_prefill_kv) and calling
+ * dsa_sparse_mla_prefill, up to the summation order (and one bf16 rounding of
+ * the cached part before the merge).
+ * Replaces, at dlengine/runtime/models/deepseek_v2/deepseek_v2.py:1573-1650, the
+ * key assembly (_gather_cache_cached_only, restore_mla_fp8_cache_rows,
+ * _interleave_cached_fresh: layers/backends/attention/mla_utils.py:118-236)
+ * followed by flash_mla_sparse_fwd. */
+DSA_API size_t dsa_sparse_mla_prefill_paged_workspace_bytes(int num_tokens, int topk);
+DSA_API int dsa_sparse_mla_prefill_paged(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                         const uint8_t* kv_cache, int64_t kv_block_stride_bytes,
+                                         int kv_block_size, int64_t kv_num_blocks,
+                                         const int32_t* block_table, int64_t bt_stride,
+                                         const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64,
+                                         int num_seqs, int64_t total_k, const void* fresh,
+                                         int64_t fresh_row_stride, int64_t total_q, const int32_t* indices,
+                                         int64_t idx_stride, int num_tokens, int num_heads, int topk,
+                                         float sm_scale, void* out, float* max_logits, float* lse,
+                                         void* workspace, size_t workspace_bytes, void* stream);
+
+
 /* Per-query key windows of a ragged prefill batch, computed on the device.
  *   cu_seqlens_q/_k [num_seqs + 1] int32 (cu_is_64 = 0) or int64: sequence b's
  *              fresh queries are the last q_len of its k_len keys

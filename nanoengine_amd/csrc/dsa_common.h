@@ -126,6 +126,16 @@ int launch_list_select(const RowRepair& rp, const int32_t* seq_lens, int64_t max
                        const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
                        int32_t* out_page, int32_t* out_raw, int top_k, int rows, hipStream_t stream);
 
+// Sparse MLA decode over physical slots of the paged fp8 cache (the body of
+// dsa_sparse_mla_decode). max_out (splits == 1 only) receives each head's
+// largest scaled score in natural units; with compact set, each row's valid
+// indices must come first and a workgroup stops at its first block with none.
+int sparse_mla_decode_impl(const void* q, int64_t q_token_stride, int64_t q_head_stride, const uint8_t* kv_cache,
+                           int64_t kv_block_stride_bytes, int kv_block_size, int64_t kv_num_blocks,
+                           const int32_t* indices, int64_t idx_stride, int num_tokens, int num_heads, int topk,
+                           float sm_scale, void* out, float* lse, int num_splits, void* workspace,
+                           size_t workspace_bytes, void* stream, float* max_out, int compact);
+
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, 64);

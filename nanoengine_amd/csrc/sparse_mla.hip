@@ -107,6 +107,8 @@ struct MlaParams {
   float* lse;
   float* ws_o;    // [splits, T, H, 512] (splits > 1)
   float* ws_lse;  // [splits, T, H]
+  float* max_out; // [T, H] largest scaled score (natural units), or null (splits == 1 only)
+  int compact;    // the valid indices of a row come first: stop at the first block with none
 };
 
 // ---- asynchronous global -> LDS copies. They are issued from inline asm so
@@ -337,6 +339,7 @@ sparse_mla_kernel(const MlaParams P) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
   float m_run = -__builtin_inff();  // per head c32, log2 domain (identical in the 4 waves of a head half)
+  float m_max = -__builtin_inff();  // exact running maximum (log2 domain), for max_out
   float l_run = 0.f;                // per head c32: this lane's 8 keys of each block only
 
   const int my_dma = dma_count(wave);
@@ -369,6 +372,8 @@ sparse_mla_kernel(const MlaParams P) {
     const uint8_t* buf = smem + (n % kNumBufs) * kBufBytes;
     const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kRingOff + (n % kRingSlots) * 256)[lane];
     const uint64_t vmask = __ballot(slot_valid(P, slot_n));
+    // every wave reads the same indices, so all of them leave at the same block
+    if (P.compact && vmask == 0ull) break;
     if (wave == kIdxWave && n + 4 < nblk) issue_index(P, smem, t, key_begin, n + 4, lane);
     // row addresses of block n+2 (its indices landed before the last barrier), read after B3
     if (wave == kTabWave && n + 2 < nblk) build_addr_table(P, smem, n + 2, lane);
@@ -463,6 +468,7 @@ sparse_mla_kernel(const MlaParams P) {
     {
       const v4f m4 = *reinterpret_cast<const v4f*>(mx);
       const float mblk = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])) * P.scale_log2;
+      m_max = fmaxf(m_max, mblk);
       const bool need = mblk > m_run + kRescaleThreshold;  // true on the first valid block
       if (__ballot(need)) {
         const float m_new = need ? mblk : m_run;
@@ -581,6 +587,8 @@ sparse_mla_kernel(const MlaParams P) {
       }
     }
     if (h == 0 && jt == 0 && head_ok && P.lse) P.lse[(int64_t)t * P.H + head] = lse;
+    if (h == 0 && jt == 0 && head_ok && P.max_out)
+      P.max_out[(int64_t)t * P.H + head] = any ? m_max * kLn2 : -__builtin_inff();
   } else {
     const int64_t row0 = ((int64_t)split * P.T + t) * P.H + h_half;
 #pragma unroll
@@ -657,7 +665,20 @@ int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_
                           int64_t kv_num_blocks, const int32_t* indices, int64_t idx_stride, int num_tokens,
                           int num_heads, int topk, float sm_scale, void* out, float* lse, int num_splits,
                           void* workspace, size_t workspace_bytes, void* stream) {
-  using namespace dsa;
+  return dsa::sparse_mla_decode_impl(q, q_token_stride, q_head_stride, kv_cache, kv_block_stride_bytes,
+                                     kv_block_size, kv_num_blocks, indices, idx_stride, num_tokens, num_heads, topk,
+                                     sm_scale, out, lse, num_splits, workspace, workspace_bytes, stream, nullptr, 0);
+}
+
+}  // extern "C"
+
+namespace dsa {
+
+int sparse_mla_decode_impl(const void* q, int64_t q_token_stride, int64_t q_head_stride, const uint8_t* kv_cache,
+                           int64_t kv_block_stride_bytes, int kv_block_size, int64_t kv_num_blocks,
+                           const int32_t* indices, int64_t idx_stride, int num_tokens, int num_heads, int topk,
+                           float sm_scale, void* out, float* lse, int num_splits, void* workspace,
+                           size_t workspace_bytes, void* stream, float* max_out, int compact) {
   if (num_tokens < 0 || num_heads <= 0 || (num_heads % 16) != 0)
     return set_error(kUnsupported, "sparse_mla: num_heads=%d must be a positive multiple of 16", num_heads);
   if (topk <= 0 || topk % kMlaKeys != 0)
@@ -717,6 +738,8 @@ int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_
   P.lse = lse;
   P.ws_o = nullptr;
   P.ws_lse = nullptr;
+  P.max_out = num_splits == 1 ? max_out : nullptr;
+  P.compact = compact;
   if (num_splits > 1) {
     const size_t rows = (size_t)num_splits * num_tokens * num_heads;
     P.ws_o = static_cast<float*>(workspace);
@@ -734,4 +757,4 @@ int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_
   return kOk;
 }
 
-}  // extern "C"
+}  // namespace dsa

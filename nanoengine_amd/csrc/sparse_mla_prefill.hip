@@ -82,6 +82,8 @@ struct PrParams {
   uint16_t* out;
   float* max_logits;
   float* lse;
+  int compact;  // the valid indices of a row come first: stop at the first block with none
+  int merge;    // combine with the (out, lse, max_logits) already stored for these rows
 };
 
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
@@ -210,6 +212,8 @@ sparse_mla_prefill_kernel(const PrParams P) {
     const uint8_t* buf = smem + (n % kPrNumBufs) * kPrBufBytes;
     const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kPrRingOff + (n % kPrRingSlots) * 128)[c32];
     const uint32_t vmask = (uint32_t)__ballot(slot_n >= 0 && (int64_t)slot_n < P.s_kv);
+    // every wave reads the same indices, so all of them leave at the same block
+    if (P.compact && vmask == 0u) break;
     if (wave == kIdxWave && n + 4 < nblk) issue_index(P, smem, t, n + 4, lane);
 
     // ---- partial S^T[32 keys x 32 heads]: s[r] = key 8(r/4) + 4h + r%4, head c32.
@@ -319,6 +323,13 @@ sparse_mla_prefill_kernel(const PrParams P) {
   }
 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // merge mode: this row's earlier result, read by every wave before the
+  // barriers below, after which one lane per head overwrites it
+  float lse_prev = -__builtin_inff(), max_prev = -__builtin_inff();
+  if (P.merge && head_ok) {
+    lse_prev = P.lse[(int64_t)t * P.H + head];
+    max_prev = P.max_logits[(int64_t)t * P.H + head];
+  }
   l_run += shfl_xor(l_run, 32);
   barrier();
   if (h == 0) mx[q4] = l_run;
@@ -330,24 +341,123 @@ sparse_mla_prefill_kernel(const PrParams P) {
   if (h_half >= P.H) return;
   const bool any = l_run > 0.f;
   const float inv = any ? 1.f / l_run : 0.f;
+  float lse_new = any ? (m_run + __builtin_amdgcn_logf(l_run)) * kLn2 : -__builtin_inff();
+  float max_new = any ? m_max * kLn2 : -__builtin_inff();
+  // weights of the earlier and of this result (merge_attention_states' LSE rule)
+  float w_prev = 0.f, w_this = 1.f;
+  if (P.merge) {
+    const float m = fmaxf(lse_prev, lse_new);
+    if (m == -__builtin_inff()) {
+      w_prev = 0.f;
+      w_this = 0.f;
+    } else {
+      const float a = __expf(lse_prev - m), b = __expf(lse_new - m);
+      w_prev = a / (a + b);
+      w_this = b / (a + b);
+      lse_new = m + __logf(a + b);
+    }
+    max_new = fmaxf(max_new, max_prev);
+  }
   // o[nt][r]: head h_half + 8(r/4) + 4h + r%4, dim 128 q4 + 32nt + c32
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
-    const float ir = __shfl(inv, hr, 64);
+    const float ir = __shfl(inv * w_this, hr, 64);
+    const float wp = __shfl(w_prev, hr, 64);
     if (h_half + hr < P.H) {
       uint16_t* orow = P.out + ((int64_t)t * P.H + h_half + hr) * kPrDv + 128 * q4 + c32;
+      if (P.merge) {
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
+        for (int nt = 0; nt < 4; ++nt)
+          orow[32 * nt] = (uint16_t)f32_to_bf16_rne(fmaf(wp, bf16_to_f32(orow[32 * nt]), o[nt][r] * ir));
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
+      }
     }
   }
   if (h == 0 && q4 == 0 && head_ok) {
-    if (P.lse) P.lse[(int64_t)t * P.H + head] = any ? (m_run + __builtin_amdgcn_logf(l_run)) * kLn2 : -__builtin_inff();
-    if (P.max_logits) P.max_logits[(int64_t)t * P.H + head] = any ? m_max * kLn2 : -__builtin_inff();
+    if (P.lse) P.lse[(int64_t)t * P.H + head] = lse_new;
+    if (P.max_logits) P.max_logits[(int64_t)t * P.H + head] = max_new;
   }
 }
 
+// The chunked prefill's top-k split by where each key lives. Index g of token t
+// is a position in the ragged key order (sequence b's keys at cu_k[b] ..): key
+// i = g - cu_k[b] is cached row i of sequence b while i < k_len - q_len (its
+// physical slot block_table[b][i / bs] * bs + i % bs in the paged fp8 cache),
+// else fresh row cu_q[b] + i - (k_len - q_len). Each token's two lists are
+// compacted in index order and padded with -1 to their widths. One 256-thread
+// workgroup per token.
+__global__ void __launch_bounds__(256)
+prefill_split_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int topk, const void* __restrict__ cu_q,
+                     const void* __restrict__ cu_k, int cu_is_64, int num_seqs, int64_t total_k,
+                     const int32_t* __restrict__ bt, int64_t bt_stride, int block_size,
+                     int32_t* __restrict__ cached, int cached_w, int32_t* __restrict__ fresh, int fresh_w) {
+  auto cu = [&](const void* p, int i) -> int64_t {
+    return cu_is_64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
+  };
+  __shared__ int s_cnt[2][4];
+  __shared__ int s_base[2];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t* row = idx + (int64_t)t * idx_stride;
+  int32_t* crow = cached + (int64_t)t * cached_w;
+  int32_t* frow = fresh + (int64_t)t * fresh_w;
+  if (tid == 0) s_base[0] = s_base[1] = 0;
+  for (int e0 = 0; e0 < topk; e0 += 256) {
+    const int e = e0 + tid;
+    int kind = -1;  // 0 cached, 1 fresh
+    int32_t v = -1;
+    const int64_t g = e < topk ? (int64_t)row[e] : -1;
+    if (g >= 0 && g < total_k) {
+      int lo = 0, hi = num_seqs;  // largest b < num_seqs with cu_k[b] <= g
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (cu(cu_k, mid) <= g) lo = mid; else hi = mid;
+      }
+      const int64_t k0 = cu(cu_k, lo), k1 = cu(cu_k, lo + 1);
+      const int64_t ncached = (k1 - k0) - (cu(cu_q, lo + 1) - cu(cu_q, lo));
+      const int64_t i = g - k0;
+      if (i < ncached) {
+        kind = 0;
+        v = bt[(int64_t)lo * bt_stride + i / block_size] * block_size + (int32_t)(i % block_size);
+      } else {
+        kind = 1;
+        v = (int32_t)(cu(cu_q, lo) + i - ncached);
+      }
+    }
+    const uint64_t mc = __ballot(kind == 0), mf = __ballot(kind == 1);
+    if (lane == 0) {
+      s_cnt[0][wave] = __popcll(mc);
+      s_cnt[1][wave] = __popcll(mf);
+    }
+    __syncthreads();
+    int bc = s_base[0], bf = s_base[1];
+    for (int w = 0; w < wave; ++w) {
+      bc += s_cnt[0][w];
+      bf += s_cnt[1][w];
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    if (kind == 0) crow[bc + __popcll(mc & below)] = v;
+    if (kind == 1) frow[bf + __popcll(mf & below)] = v;
+    __syncthreads();
+    if (tid == 0) {
+      s_base[0] += s_cnt[0][0] + s_cnt[0][1] + s_cnt[0][2] + s_cnt[0][3];
+      s_base[1] += s_cnt[1][0] + s_cnt[1][1] + s_cnt[1][2] + s_cnt[1][3];
+    }
+    __syncthreads();
+  }
+  const int nc = s_base[0], nf = s_base[1];
+  for (int e = nc + tid; e < cached_w; e += 256) crow[e] = -1;
+  for (int e = nf + tid; e < fresh_w; e += 256) frow[e] = -1;
+}
+
 }  // namespace
+
+static int sparse_mla_prefill_impl(const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* kv,
+                                   int64_t kv_row_stride, int64_t s_kv, const int32_t* indices, int64_t idx_stride,
+                                   int num_tokens, int num_heads, int topk, float sm_scale, void* out,
+                                   float* max_logits, float* lse, void* stream, int compact, int merge);
 }  // namespace dsa
 
 extern "C" {
@@ -356,7 +466,19 @@ int dsa_sparse_mla_prefill(const void* q, int64_t q_token_stride, int64_t q_head
                            int64_t kv_row_stride, int64_t s_kv, const int32_t* indices, int64_t idx_stride,
                            int num_tokens, int num_heads, int topk, float sm_scale, void* out, float* max_logits,
                            float* lse, void* stream) {
-  using namespace dsa;
+  return dsa::sparse_mla_prefill_impl(q, q_token_stride, q_head_stride, kv, kv_row_stride, s_kv, indices,
+                                      idx_stride, num_tokens, num_heads, topk, sm_scale, out, max_logits, lse,
+                                      stream, 0, 0);
+}
+
+}  // extern "C"
+
+namespace dsa {
+
+static int sparse_mla_prefill_impl(const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* kv,
+                                   int64_t kv_row_stride, int64_t s_kv, const int32_t* indices, int64_t idx_stride,
+                                   int num_tokens, int num_heads, int topk, float sm_scale, void* out,
+                                   float* max_logits, float* lse, void* stream, int compact, int merge) {
   if (num_tokens < 0 || num_heads <= 0 || (num_heads % 16) != 0)
     return set_error(kUnsupported, "sparse_mla_prefill: num_heads=%d must be a positive multiple of 16", num_heads);
   if (topk <= 0 || topk % kPrKeys != 0)
@@ -393,11 +515,64 @@ int dsa_sparse_mla_prefill(const void* q, int64_t q_token_stride, int64_t q_head
   P.out = static_cast<uint16_t*>(out);
   P.max_logits = max_logits;
   P.lse = lse;
+  P.compact = compact;
+  P.merge = merge;
   const int64_t nwg = (int64_t)num_tokens * P.head_groups;
   if (nwg > INT32_MAX) return set_error(kInvalidArgument, "sparse_mla_prefill: grid too large");
   hipLaunchKernelGGL(sparse_mla_prefill_kernel, dim3((unsigned)nwg), dim3(kPrThreads), kPrSmemBytes,
                      (hipStream_t)stream, P);
   return check_launch("dsa_sparse_mla_prefill");
+}
+
+static inline size_t pf_align(size_t x) { return (x + 255) & ~(size_t)255; }
+static inline int cached_width(int topk) { return (topk + 63) / 64 * 64; }
+static inline int fresh_width(int topk) { return (topk + kPrKeys - 1) / kPrKeys * kPrKeys; }
+
+}  // namespace dsa
+
+extern "C" {
+
+size_t dsa_sparse_mla_prefill_paged_workspace_bytes(int num_tokens, int topk) {
+  using namespace dsa;
+  if (num_tokens <= 0 || topk <= 0) return 0;
+  return pf_align((size_t)num_tokens * cached_width(topk) * 4) + pf_align((size_t)num_tokens * fresh_width(topk) * 4);
+}
+
+int dsa_sparse_mla_prefill_paged(const void* q, int64_t q_token_stride, int64_t q_head_stride,
+                                 const uint8_t* kv_cache, int64_t kv_block_stride_bytes, int kv_block_size,
+                                 int64_t kv_num_blocks, const int32_t* block_table, int64_t bt_stride,
+                                 const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64, int num_seqs,
+                                 int64_t total_k, const void* fresh, int64_t fresh_row_stride, int64_t total_q,
+                                 const int32_t* indices, int64_t idx_stride, int num_tokens, int num_heads, int topk,
+                                 float sm_scale, void* out, float* max_logits, float* lse, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  using namespace dsa;
+  if (num_tokens < 0 || num_seqs < 1 || total_k < 0 || total_q < 0 || topk <= 0 || kv_block_size <= 0)
+    return set_error(kInvalidArgument, "sparse_mla_prefill_paged: bad sizes");
+  if (num_tokens == 0) return kOk;
+  if (!indices || !block_table || !cu_seqlens_q || !cu_seqlens_k || !out || !max_logits || !lse || !workspace)
+    return set_error(kInvalidArgument, "sparse_mla_prefill_paged: null pointer");
+  const size_t need = dsa_sparse_mla_prefill_paged_workspace_bytes(num_tokens, topk);
+  if (workspace_bytes < need)
+    return set_error(kWorkspaceTooSmall, "sparse_mla_prefill_paged: workspace %zu B < %zu B", workspace_bytes, need);
+  const int cw = cached_width(topk), fw = fresh_width(topk);
+  int32_t* cached = static_cast<int32_t*>(workspace);
+  int32_t* fresh_idx =
+      reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + pf_align((size_t)num_tokens * cw * 4));
+  hipStream_t st = (hipStream_t)stream;
+  // 1. each token's indices split into cache slots and fresh rows, compacted
+  hipLaunchKernelGGL(prefill_split_kernel, dim3((unsigned)num_tokens), dim3(256), 0, st, indices, idx_stride, topk,
+                     cu_seqlens_q, cu_seqlens_k, cu_is_64, num_seqs, total_k, block_table, bt_stride, kv_block_size,
+                     cached, cw, fresh_idx, fw);
+  if (int rc = check_launch("dsa_sparse_mla_prefill_paged(split)")) return rc;
+  // 2. the cached keys straight from the paged fp8 cache, exact dequantisation in registers
+  if (int rc = sparse_mla_decode_impl(q, q_token_stride, q_head_stride, kv_cache, kv_block_stride_bytes, kv_block_size,
+                                      kv_num_blocks, cached, cw, num_tokens, num_heads, cw, sm_scale, out, lse, 1,
+                                      nullptr, 0, stream, max_logits, 1))
+    return rc;
+  // 3. the fresh bf16 rows, merged into that result by LSE
+  return sparse_mla_prefill_impl(q, q_token_stride, q_head_stride, fresh, fresh_row_stride, total_q, fresh_idx, fw,
+                                 num_tokens, num_heads, fw, sm_scale, out, max_logits, lse, stream, 1, 1);
 }
 
 }  // extern "C"

@@ -96,3 +96,31 @@ def flash_mla_sparse_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tenso
     if idx.stride(-1) != 1:
         idx = idx.contiguous()
     return ops.sparse_mla_prefill(q, kv[:, 0, :], idx, sm_scale)
+
+
+def flash_mla_sparse_fwd_paged(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor,
+                               cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, key_states: torch.Tensor,
+                               indices: torch.Tensor, sm_scale: float, d_v: int = 512,
+                               total_k: int | None = None):
+    """The chunked prefill's key assembly and sparse MLA in one call
+    (models/deepseek_v2/deepseek_v2.py:1573-1650: _gather_cache_cached_only,
+    restore_mla_fp8_cache_rows and _interleave_cached_fresh, then
+    flash_mla_sparse_fwd): the cached keys are read from the paged fp8 cache,
+    the fresh ones from key_states [total_q, (1,) 576] bf16. indices
+    [s_q, 1, topk] are positions in the ragged key order. Returns
+    (out [s_q, h_q, d_v] bf16, max_logits [s_q, h_q] f32, lse [s_q, h_q] f32)."""
+    if d_v != ops.MLA_D_V:
+        raise ValueError(f"d_v must be {ops.MLA_D_V}, got {d_v}")
+    if indices.dim() != 3 or indices.shape[1] != 1 or indices.shape[0] != q.shape[0]:
+        raise ValueError(f"indices must be [s_q, 1, topk], got {tuple(indices.shape)}")
+    idx = indices[:, 0, :]
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    if idx.stride(-1) != 1:
+        idx = idx.contiguous()
+    if total_k is None:
+        total_k = int(cu_seqlens_k[-1].item())
+    dt = torch.int64 if torch.int64 in (cu_seqlens_q.dtype, cu_seqlens_k.dtype) else torch.int32
+    bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+    return ops.sparse_mla_prefill_paged(q, k_cache, bt, cu_seqlens_q.to(dt).contiguous(),
+                                        cu_seqlens_k.to(dt).contiguous(), key_states, idx, sm_scale, total_k)

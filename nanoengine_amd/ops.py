@@ -579,3 +579,57 @@ def sparse_mla_prefill(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor,
               kv2.shape[0], indices.data_ptr(), indices.stride(0), T, H, topk, float(sm_scale), out.data_ptr(),
               max_logits.data_ptr(), lse.data_ptr(), _stream(dev))
     return out, max_logits, lse
+
+
+def sparse_mla_prefill_paged_workspace_bytes(num_tokens: int, topk: int) -> int:
+    return int(_lib.load().dsa_sparse_mla_prefill_paged_workspace_bytes(num_tokens, topk))
+
+
+def sparse_mla_prefill_paged(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor,
+                             cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, fresh: torch.Tensor,
+                             indices: torch.Tensor, sm_scale: float, total_k: int,
+                             out: torch.Tensor | None = None, max_logits: torch.Tensor | None = None,
+                             lse: torch.Tensor | None = None, workspace: torch.Tensor | None = None):
+    """Sparse MLA prefill with the cached keys read from the paged fp8 cache and
+    the fresh keys from bf16 rows (see dsa_sparse_mla_prefill_paged). indices
+    [T, topk] int32 are positions in the ragged key order of total_k keys.
+    Returns (out [T, H, 512] bf16, max_logits [T, H] f32, lse [T, H] f32)."""
+    _require(q.dim() == 3 and q.shape[2] == MLA_D_QK and q.dtype == torch.bfloat16 and q.stride(2) == 1,
+             f"q must be bf16 [T, H, 576] with a contiguous last dim, got {tuple(q.shape)} {q.dtype}", ValueError)
+    blk_stride, block_size = mla_kv_geometry(k_cache)
+    T, H, _ = q.shape
+    _require(indices.dim() == 2 and indices.shape[0] == T and indices.dtype == torch.int32
+             and indices.stride(1) == 1, "indices must be int32 [T, topk]", ValueError)
+    _require(cu_seqlens_q.dtype == cu_seqlens_k.dtype and cu_seqlens_q.dtype in (torch.int32, torch.int64)
+             and cu_seqlens_q.shape == cu_seqlens_k.shape and cu_seqlens_q.dim() == 1
+             and cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous(),
+             "cu_seqlens_q/_k must be contiguous int32 or int64 [num_seqs + 1] of one dtype", ValueError)
+    num_seqs = cu_seqlens_q.numel() - 1
+    _require(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == num_seqs
+             and block_table.stride(1) == 1, "block_table must be int32 [num_seqs, M]", ValueError)
+    f2 = fresh.reshape(fresh.shape[0], -1) if fresh.dim() == 3 else fresh
+    _require(f2.dim() == 2 and f2.shape[1] == MLA_D_QK and f2.dtype == torch.bfloat16 and f2.stride(1) == 1,
+             "fresh must be bf16 [total_q, 576]", ValueError)
+    topk = indices.shape[1]
+    dev = _check_cuda(q, k_cache, block_table, cu_seqlens_q, cu_seqlens_k, f2, indices)
+    if out is None:
+        out = torch.empty(T, H, MLA_D_V, dtype=torch.bfloat16, device=dev)
+    if max_logits is None:
+        max_logits = torch.empty(T, H, dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty(T, H, dtype=torch.float32, device=dev)
+    _require(out.shape == (T, H, MLA_D_V) and out.dtype == torch.bfloat16 and out.is_contiguous(),
+             "out must be contiguous bf16 [T, H, 512]", ValueError)
+    for t_, nm in ((max_logits, "max_logits"), (lse, "lse")):
+        _require(t_.shape == (T, H) and t_.dtype == torch.float32 and t_.is_contiguous(),
+                 f"{nm} must be contiguous f32 [T, H]", ValueError)
+    need = sparse_mla_prefill_paged_workspace_bytes(T, topk)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    _lib.call("dsa_sparse_mla_prefill_paged", q.data_ptr(), q.stride(0), q.stride(1), _as_bytes(k_cache).data_ptr(),
+              blk_stride, block_size, k_cache.shape[0], block_table.data_ptr(), block_table.stride(0),
+              cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), int(cu_seqlens_q.dtype == torch.int64), num_seqs,
+              int(total_k), f2.data_ptr(), f2.stride(0), f2.shape[0], indices.data_ptr(), indices.stride(0), T, H,
+              topk, float(sm_scale), out.data_ptr(), max_logits.data_ptr(), lse.data_ptr(), workspace.data_ptr(),
+              workspace.numel(), _stream(dev))
+    return out, max_logits, lse

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import oracle as O
-from nanoengine_amd import mla_utils, synth
+from nanoengine_amd import mla_utils, ops, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -36,3 +36,73 @@ def test_assemble_prefill_kv_matches_oracle(cuda, cu_dtype):
     exp = O.assemble_prefill_kv(rows, 64, bt, cu_q, cu_k, fresh.float().cpu().numpy())
     assert out.shape == (int(cu_k[-1]), 1, 576)
     assert np.array_equal(out[:, 0].float().cpu().numpy(), exp)
+
+
+def _paged_case(cuda, seed=7, H=128, topk=256):
+    rng = np.random.default_rng(seed)
+    q_lens = np.array([40, 0, 129, 64, 3])
+    k_lens = q_lens + np.array([300, 70, 0, 1000, 4000])
+    pages = (k_lens + 63) // 64
+    num_blocks = int(pages.sum()) + 5
+    perm = rng.permutation(num_blocks)
+    bt = np.zeros((len(q_lens), pages.max()), np.int32)
+    at = 0
+    for b, p in enumerate(pages):
+        bt[b, :p] = perm[at:at + p]
+        at += p
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)])
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)])
+    T, total_k = int(cu_q[-1]), int(cu_k[-1])
+    idx = np.full((T, topk), -1, np.int32)
+    for b in range(len(q_lens)):
+        cached = k_lens[b] - q_lens[b]
+        for j in range(q_lens[b]):
+            t = cu_q[b] + j
+            win = cached + j + 1
+            n = min(topk, win)
+            sel = rng.choice(win, size=n, replace=False) + cu_k[b]
+            idx[t, :n] = sel
+            if n < topk:
+                idx[t, n] = total_k + 5          # out of range: skipped
+    idx[cu_q[3] + 1] = -1                        # a token with no valid index
+    kv = synth.make_mla_cache(num_blocks, seed=seed, device=cuda)
+    g = torch.Generator(device=cuda).manual_seed(seed)
+    fresh = torch.randn(T, 576, device=cuda, generator=g).to(torch.bfloat16)
+    q = synth.make_mla_query(T, H, seed=seed, device=cuda)
+    t32 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda, torch.int32)   # noqa: E731
+    return q, kv, t32(bt), t32(cu_q), t32(cu_k), fresh, t32(idx), total_k, (bt, cu_q, cu_k, idx)
+
+
+def test_paged_prefill_matches_assembled_rows(cuda):
+    """The paged sparse prefill (cached keys from the fp8 cache through the
+    decode kernel, fresh keys as bf16 rows, LSE merge) against the assembled
+    bf16 keys through the bf16 prefill kernel and against the oracle; the
+    sequences include one with no cached prefix, a token with no valid index
+    and indices past the key count."""
+    print("paged sparse prefill", flush=True)
+    q, kv, bt, cu_q, cu_k, fresh, idx, total_k, host = _paged_case(cuda)
+    scale = 192 ** -0.5
+    o, mx, lse = ops.sparse_mla_prefill_paged(q, kv, bt, cu_q, cu_k, fresh, idx, scale, total_k)
+    asm = mla_utils.assemble_prefill_kv(kv, bt, cu_q, cu_k, fresh.unsqueeze(1), total_k)[:, 0]
+    eo, emx, else_ = ops.sparse_mla_prefill(q, asm, idx, scale)
+    torch.cuda.synchronize()
+    # two GPU results, each rounded to bf16 on its own (the paged one also rounds
+    # the cached part before the merge): a bf16 ulp of the value on top of atol
+    assert torch.all((o.float() - eo.float()).abs() <= 2e-2 + eo.float().abs() * 2.0 ** -7)
+    fin = torch.isfinite(else_)
+    assert torch.equal(torch.isfinite(lse), fin) and torch.equal(torch.isfinite(mx), torch.isfinite(emx))
+    assert (lse[fin] - else_[fin]).abs().max().item() <= 1e-3
+    assert (mx[fin] - emx[fin]).abs().max().item() <= 1e-3
+    bt_h, cu_q_h, cu_k_h, idx_h = host
+    rows = kv.contiguous().reshape(-1, 656).cpu().numpy()
+    kv_or = O.assemble_prefill_kv(rows, 64, bt_h, cu_q_h, cu_k_h, fresh.float().cpu().numpy())
+    sample = np.array([0, 39, 40, 100, 168, 200, int(cu_q_h[3]) + 1, int(cu_q_h[-1]) - 1])
+    oo, omx, olse = O.sparse_mla_prefill(q[sample].float().cpu().numpy(), kv_or, idx_h[sample], scale)
+    err = np.abs(o[sample].float().cpu().numpy() - oo)
+    print(f"paged prefill vs oracle: max |o err| {err.max():.4f} at |o| {np.abs(oo).flat[err.argmax()]:.3f}", flush=True)
+    assert err.max() <= 2e-2
+    ofin = np.isfinite(olse)
+    assert np.array_equal(np.isfinite(lse[sample].cpu().numpy()), ofin)
+    assert np.abs(lse[sample].cpu().numpy()[ofin] - olse[ofin]).max() <= 1e-3
+    assert np.abs(mx[sample].cpu().numpy()[ofin] - omx[ofin]).max() <= 1e-3
+    assert torch.all(o[int(cu_q_h[3]) + 1] == 0)
