@@ -167,6 +167,11 @@ sparse_mla_prefill_kernel(const PrParams P) {
   const int h_half = hg * kPrHeadsPerWG + hp * 32;
   const int head = h_half + c32;
   const bool head_ok = head < P.H;
+  // merging a compacted list that is empty leaves the stored result as it is
+  if (P.compact && P.merge) {
+    const int32_t first = P.idx[(int64_t)t * P.idx_stride];
+    if (first < 0 || (int64_t)first >= P.s_kv) return;
+  }
 
   // query B operands: k-step ks of the nope quarter = dims 128q + 16ks + 8h .. +8,
   // rope = dims 512 + 16q + 8h .. +8, of head c32
