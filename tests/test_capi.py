@@ -87,3 +87,31 @@ def test_workspace_size_queries(lib):
     assert lib.dsa_sparse_mla_num_splits(128, 128, 2048, 256) == 1
     assert lib.dsa_sparse_mla_num_splits(32, 128, 2048, 256) == 4
     assert lib.dsa_sparse_mla_num_splits(1, 16, 128, 256) == 2
+
+
+def test_prefill_entry_points_reject_bad_arguments(lib):
+    P = None
+    # prefill windows: at least one sequence, non-negative sizes, pointers
+    assert lib.dsa_prefill_windows(P, P, 0, 0, 4, 64, P, P, P, P) == 1
+    assert lib.dsa_prefill_windows(P, P, 0, 2, 4, 0, P, P, P, P) == 1
+    assert b"null pointer" in (lib.dsa_prefill_windows(P, P, 0, 2, 4, 64, P, P, P, P) == 1 and lib.dsa_last_error())
+    # key assembly: rows of 576, a block stride that holds the block's rows, 16-byte alignment
+    assert lib.dsa_mla_prefill_kv(P, 64 * 656 - 1, 64, P, 0, P, P, 0, 1, 10, P, 576, P, 576, P) == 1
+    assert lib.dsa_mla_prefill_kv(P, 42640, 64, P, 0, P, P, 0, 1, 10, P, 512, P, 576, P) == 1
+    assert lib.dsa_mla_prefill_kv(P, 42640, 64, P, 0, P, P, 0, 1, 0, P, 576, P, 576, P) == 0   # nothing to do
+    # paged sparse prefill: workspace sizing and the workspace check come before any launch
+    assert lib.dsa_sparse_mla_prefill_paged_workspace_bytes(8192, 2048) == 2 * 8192 * 2048 * 4
+    assert lib.dsa_sparse_mla_prefill_paged_workspace_bytes(0, 2048) == 0
+    ws = lib.dsa_sparse_mla_prefill_paged_workspace_bytes(10, 2048)
+    f = ctypes.c_float(0.1)
+    one = ctypes.c_void_p(16)  # a non-null address that is never dereferenced
+    args = [one, 0, 0, one, 42640, 64, 10, one, 0, one, one, 0, 1, 100, one, 576, 10, one, 2048, 10, 128, 2048,
+            f, one, one, one, one]
+    assert lib.dsa_sparse_mla_prefill_paged(*args, ws - 1, P) == 4          # workspace too small
+    assert b"workspace" in lib.dsa_last_error()
+    bad = list(args)
+    bad[12] = 0                                                             # no sequences
+    assert lib.dsa_sparse_mla_prefill_paged(*bad, ws, P) == 1
+    bad = list(args)
+    bad[26] = P                                                             # no workspace
+    assert lib.dsa_sparse_mla_prefill_paged(*bad, ws, P) == 1
