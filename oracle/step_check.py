@@ -121,18 +121,20 @@ def check_step_rows(*, q_idx, idx_pages, weights, ctx, bt_local, bt_global, max_
 
 
 def sample_from_device(rows, *, q_idx_fp8, weights, cache, lens, block_tables, q_mla, kv, logits,
-                       logical, physical, o, lse, page_size=64) -> dict:
+                       logical, physical, o, lse, page_size=64, next_n=1) -> dict:
     """Copies what :func:`check_step_rows` needs for ``rows`` from the GPU
     step's tensors (torch, on the device) to host numpy: the rows' indexer
     pages (densely renumbered), their query, weights and tables, the GPU's
     logits, indices and outputs, and the MLA cache rows at the GPU's physical
-    indices. ``kv`` is the [blocks, 64, 1, 656] cache view."""
+    indices. ``kv`` is the [blocks, 64, 1, 656] cache view. Rows are query
+    tokens: with ``next_n`` > 1 row r is draft position r % next_n of sequence
+    r // next_n, and ``lens`` holds each query token's own causal length."""
     import torch
 
     dev = q_idx_fp8.device
     rt = torch.as_tensor(np.asarray(rows), dtype=torch.long, device=dev)
     ctx = np.asarray([int(lens[int(r)]) for r in rows], dtype=np.int32)
-    bt_global = block_tables.index_select(0, rt).cpu().numpy()
+    bt_global = block_tables.index_select(0, rt // next_n).cpu().numpy()
     used, bt_local = localize_pages(bt_global, ctx, page_size)
     pages = cache.index_select(0, torch.as_tensor(used, dtype=torch.long, device=dev)).cpu().numpy()
     phys = physical.index_select(0, rt)

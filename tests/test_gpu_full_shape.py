@@ -1,0 +1,81 @@
+"""The decode step at the BASELINE shapes, checked against the CPU oracle.
+
+Config 2 at its own shape: the fused decode step over B=128 sequences of 64K
+context (top-2048, 128 MLA heads), exactly as bench.py builds
+it, with 12 rows spread over the batch (and therefore over the persistent
+filter's contiguous per-wave page ranges and the XCDs) checked against the CPU
+oracle: logits within 1e-3 relative, logical top-2048 bit-exact against the
+exact selection over the GPU logits (and tie-only differences against the
+oracle's float64 logits), physical slots bit-exact, MLA o within atol 2e-2 and
+LSE within 1e-3."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import step_check as SC
+from nanoengine_amd import ops, synth
+from nanoengine_amd.pipeline import DsaDecodeStep
+
+pytestmark = pytest.mark.gpu
+
+
+def test_config2_full_step_sampled_rows_match_oracle(cuda):
+    B, L, H, K, seed = 128, 65536, 128, 2048, 0
+    print(f"config2 B={B} L={L} H={H} K={K} seed={seed}", flush=True)
+    lens = [L] * B
+    inp = synth.make_indexer_inputs(lens, next_n=1, seed=seed, device=cuda)
+    kv = synth.make_mla_cache(int(inp.block_tables.max().item()) + 1, seed=seed, device=cuda)
+    q_mla = synth.make_mla_query(B, H, seed=seed, device=cuda)
+    max_ctx = inp.block_tables.shape[1] * 64
+    step = DsaDecodeStep(B, 1, max_ctx, num_heads=H, index_topk=K, device=cuda)
+    seq = step.expand_lens(inp.context_lens)
+    o, lse, logical, physical = step(inp.q_fp8, inp.weights, inp.cache, seq, inp.block_tables, inp.block_tables,
+                                     q_mla, kv, 192 ** -0.5)
+    logits = ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1),
+                                inp.block_tables, max_ctx)
+    torch.cuda.synchronize()
+    rows = SC.spread_rows(B, 12)
+    data = SC.sample_from_device(rows, q_idx_fp8=inp.q_fp8, weights=inp.weights, cache=inp.cache, lens=lens,
+                                 block_tables=inp.block_tables, q_mla=q_mla, kv=kv, logits=logits,
+                                 logical=logical, physical=physical, o=o, lse=lse)
+    rep = SC.check_step_rows(**data, sm_scale=192 ** -0.5, topk=K)
+    print(rep, flush=True)
+    assert rep["ok"], rep
+    # every row of the batch selected exactly K distinct in-range positions
+    lg = logical.cpu().numpy()
+    assert np.all((lg >= 0) & (lg < L))
+    assert np.all(np.diff(lg, axis=1) > 0)
+
+
+def test_config3_mtp_step_sampled_rows_match_oracle(cuda):
+    """BASELINE config 3 at its own shape: MTP verify with next_n = 2 over 64
+    sequences of lognormal length (median 16K, clipped to 2K-128K), built as
+    bench.py --config 3 builds it. Each query token has its own causal length
+    (ctx - 1 for the first draft position); 12 query rows spread over the batch
+    are checked against the oracle to the same bounds as config 2."""
+    B, n, H, K, seed = 64, 2, 128, 2048, 0
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in np.clip(np.exp(rng.normal(np.log(16384), 1.0, B)), 2048, 131072)]
+    print(f"config3 B={B} n={n} H={H} K={K} seed={seed} max_len={max(lens)}", flush=True)
+    inp = synth.make_indexer_inputs(lens, next_n=n, seed=seed, device=cuda)
+    kv = synth.make_mla_cache(int(inp.block_tables.max().item()) + 1, seed=seed, device=cuda)
+    q_mla = synth.make_mla_query(B * n, H, seed=seed, device=cuda)
+    max_ctx = inp.block_tables.shape[1] * 64
+    step = DsaDecodeStep(B, n, max_ctx, num_heads=H, index_topk=K, device=cuda)
+    seq = step.expand_lens(inp.context_lens)
+    pt = inp.block_tables.repeat_interleave(n, dim=0).contiguous()
+    o, lse, logical, physical = step(inp.q_fp8, inp.weights, inp.cache, seq, inp.block_tables, pt, q_mla, kv,
+                                     192 ** -0.5)
+    logits = ops.indexer_logits(inp.q_fp8.view(B, n, 64, 128), inp.cache, inp.weights, seq.view(B, n),
+                                inp.block_tables, max_ctx)
+    torch.cuda.synchronize()
+    rows = SC.spread_rows(B * n, 12)
+    qlens = seq.cpu().numpy()
+    data = SC.sample_from_device(rows, q_idx_fp8=inp.q_fp8, weights=inp.weights, cache=inp.cache, lens=qlens,
+                                 block_tables=inp.block_tables, q_mla=q_mla, kv=kv, logits=logits,
+                                 logical=logical, physical=physical, o=o, lse=lse, next_n=n)
+    rep = SC.check_step_rows(**data, sm_scale=192 ** -0.5, topk=K)
+    print(rep, flush=True)
+    assert rep["ok"], rep
+    # the first draft position sees one key fewer than the second
+    assert np.all(qlens.reshape(B, n)[:, 0] == qlens.reshape(B, n)[:, 1] - 1)
