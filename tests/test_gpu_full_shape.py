@@ -79,3 +79,32 @@ def test_config3_mtp_step_sampled_rows_match_oracle(cuda):
     assert rep["ok"], rep
     # the first draft position sees one key fewer than the second
     assert np.all(qlens.reshape(B, n)[:, 0] == qlens.reshape(B, n)[:, 1] - 1)
+
+
+def test_config1_mla_alone_sampled_tokens_match_oracle(cuda):
+    """BASELINE config 1 at its own shape: sparse MLA decode alone, B=32 x 32K
+    context, 128 heads, top-2048 random positions through random block tables,
+    with the split count the library picks (key splits + LSE combine). Eight
+    tokens are checked against the oracle (o atol 2e-2, LSE 1e-3)."""
+    import oracle as O
+    from nanoengine_amd import mla_utils
+    B, L, H, K, seed = 32, 32768, 128, 2048, 0
+    print(f"config1 B={B} L={L} H={H} K={K} seed={seed}", flush=True)
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    bt, num_pages = synth.make_block_tables([L] * B, gen, cuda)
+    kv = synth.make_mla_cache(num_pages, seed=seed, device=cuda)
+    q = synth.make_mla_query(B, H, seed=seed, device=cuda)
+    pos = synth.random_topk_positions([L] * B, K, seed=seed, device=cuda)
+    idx = mla_utils.topk_indices_to_physical(pos, bt, 64)
+    splits = ops.sparse_mla_num_splits(B, H, K, cuda)
+    assert splits > 1
+    o, lse = ops.sparse_mla_decode(q, kv, idx, 192 ** -0.5, num_splits=splits)
+    torch.cuda.synchronize()
+    rows = SC.spread_rows(B, 8)
+    for r in rows.tolist():
+        sel = idx[r].long()
+        kv_sel = kv[sel // 64, sel % 64, 0].cpu().numpy()
+        eo, el = O.sparse_mla_decode(q[r:r + 1].float().cpu().numpy(), kv_sel, np.arange(K)[None, :],
+                                     192 ** -0.5)
+        assert np.abs(o[r].float().cpu().numpy() - eo[0]).max() <= 2e-2
+        assert np.abs(lse[r].cpu().numpy() - el[0]).max() <= 1e-3
