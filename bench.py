@@ -57,7 +57,7 @@ def parse_args():
                         "3: MTP verify, B=64, next_n=2, "
                         "lognormal lengths (median 16K, clipped to 2K-128K); 4: chunked prefill, "
                         "8192 queries over a 120K cached prefix (128K keys)")
-    p.add_argument("--only", choices=["fused", "indexer", "topk", "mla", "logits", "kv"], default=None,
+    p.add_argument("--only", choices=["fused", "indexer", "topk", "mla", "logits", "kv", "mlabf16"], default=None,
                    help="profiling aid: launch only this stage in the timed loop (no JSON line)")
     return p.parse_args()
 
@@ -272,11 +272,14 @@ def bench_prefill(args):
     """one 8192-token chunk over a 122880-token cached prefix
     (131072 keys in all). Stages, each timed with HIP events on the launch
     stream over `steps` repetitions: the paged-to-ragged indexer key gather,
-    the ragged fp8 MQA logits [8192 x 131072] (causal windows), the ragged
-    top-2048 and the sparse MLA prefill: the selected keys of the cached prefix
-    read from the paged fp8 MLA cache, those of the chunk's fresh keys as bf16
-    rows (dsa_sparse_mla_prefill_paged). The reference's route (the keys
-    assembled as bf16 rows, then the bf16 sparse prefill) is timed beside it."""
+    the ragged fp8 MQA logits [8192 x 131072] (causal windows) fused with the
+    exact ragged top-2048 (dsa_mqa_topk: no logits buffer), and the sparse MLA
+    prefill: the selected keys of the cached prefix read from the paged fp8
+    MLA cache, those of the chunk's fresh keys as bf16 rows
+    (dsa_sparse_mla_prefill_paged). The reference's routes are timed beside
+    them: logits into a buffer then the ragged top-k (whose indices must equal
+    the fused entry's on every row), and the keys assembled as bf16 rows then
+    the bf16 sparse prefill."""
     import numpy as np
     import torch
 
@@ -315,11 +318,14 @@ def bench_prefill(args):
     mla_lse = torch.empty(QN, H, dtype=torch.float32, device=dev)
     scale = 192 ** -0.5
     pws = torch.empty(ops.sparse_mla_prefill_paged_workspace_bytes(QN, K), dtype=torch.uint8, device=dev)
+    tws = torch.empty(ops.mqa_topk_workspace_bytes(QN, KN, K), dtype=torch.uint8, device=dev)
+    idx2 = torch.empty_like(idx)
     stages = [
         ("gather_indexer_cache", lambda: ops.gather_indexer_cache(inp.cache, inp.block_tables, cu_k, 64, KN, keys,
                                                                   scales)),
-        ("mqa_logits", lambda: ops.mqa_logits(q8, keys.view(torch.float8_e4m3fn), kvs, w, ks, ke, logits, False)),
-        ("topk_transform_ragged", lambda: ops.topk_transform_ragged(logits, lens, ks, ks, idx, K, workspace=ws)),
+        # logits and the exact top-2048 in one pass: no logits buffer
+        ("mqa_topk", lambda: ops.mqa_topk(q8, keys.view(torch.float8_e4m3fn), kvs, w, ks, ke, KN, idx, K,
+                                          workspace=tws)),
         # the cached keys straight from the paged fp8 cache, the fresh keys as bf16 rows
         ("sparse_mla_prefill_paged", lambda: ops.sparse_mla_prefill_paged(
             q_mla, kv_cache, inp.block_tables, cu_q, cu_k, fresh, idx, scale, KN, out=mla_out, max_logits=mla_max,
@@ -329,11 +335,14 @@ def bench_prefill(args):
     alt_out = torch.empty_like(mla_out)
     alt_max, alt_lse = torch.empty_like(mla_max), torch.empty_like(mla_lse)
     alternative = [
+        # the indexer as two operators over a [QN, KN] f32 logits buffer
+        ("mqa_logits", lambda: ops.mqa_logits(q8, keys.view(torch.float8_e4m3fn), kvs, w, ks, ke, logits, False)),
+        ("topk_transform_ragged", lambda: ops.topk_transform_ragged(logits, lens, ks, ks, idx2, K, workspace=ws)),
         ("mla_prefill_kv", lambda: ops.mla_prefill_kv(kv_cache, inp.block_tables, cu_q, cu_k, fresh, KN, kv_bf16)),
         ("sparse_mla_prefill", lambda: ops.sparse_mla_prefill(q_mla, kv_bf16, idx, scale, out=alt_out,
                                                               max_logits=alt_max, lse=alt_lse)),
     ]
-    only = {"logits": "mqa_logits", "mla": "sparse_mla_prefill_paged", "kv": "mla_prefill_kv",
+    only = {"logits": "mqa_logits", "topk": "mqa_topk", "mla": "sparse_mla_prefill_paged", "kv": "mla_prefill_kv",
             "mlabf16": "sparse_mla_prefill"}.get(args.only)
     for _ in range(max(1, args.warmup)):
         for _, fn in stages:
@@ -367,6 +376,11 @@ def bench_prefill(args):
         out[name] = {"us": round(e0.elapsed_time(e1) * 1e3 / steps, 1)}
     pairs = int(lens.sum().item())
     flops = 2.0 * 64 * 128 * pairs
+    ft = out["mqa_topk"]
+    ft.update({"flops": flops, "TFLOPs": round(flops / (ft["us"] * 1e-6) / 1e12, 1),
+               "fp8_mfma_frac": round(flops / (ft["us"] * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4),
+               "phases": ["prep", "sample keys", "sampled logits (1/64 of the keys)", "threshold",
+                          "logits + filter", "list select", "fix-up of deferred rows (none here)"]})
     out["mqa_logits"].update({"flops": flops, "pairs": pairs,
                               "TFLOPs": round(flops / (out["mqa_logits"]["us"] * 1e-6) / 1e12, 1),
                               "fp8_mfma_frac": round(flops / (out["mqa_logits"]["us"] * 1e-6) / 1e12
@@ -385,7 +399,11 @@ def bench_prefill(args):
                                          "stages": ["mla_prefill_kv", "sparse_mla_prefill"],
                                          "sparse_mla_prefill": out.pop("sparse_mla_prefill")}
     out["topk_transform_ragged"]["GBps"] = round(QN * KN * 4 / (out["topk_transform_ragged"]["us"] * 1e-6) / 1e9, 1)
-    mq = out["mqa_logits"]
+    out["alternative_two_step_indexer"] = {
+        "us": round(out["mqa_logits"]["us"] + out["topk_transform_ragged"]["us"], 1),
+        "stages": ["mqa_logits", "topk_transform_ragged"],
+        "mqa_logits": out.pop("mqa_logits"), "topk_transform_ragged": out.pop("topk_transform_ragged")}
+    fused_equal = bool(torch.equal(idx, idx2))
 
     base, parity = None, None
     if not args.no_cpu_baseline:
@@ -407,20 +425,28 @@ def bench_prefill(args):
         "metric": METRIC, "value": round(QN / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8+bf16", "data": "synthetic",
-        "config": {"workload": "BASELINE config 4: chunked prefill (indexer key gather + ragged fp8 MQA logits + "
-                               "ragged top-2048 + sparse MLA prefill over the paged fp8 cache and the fresh bf16 "
+        "config": {"workload": "BASELINE config 4: chunked prefill (indexer key gather + ragged fp8 MQA logits "
+                               "fused with the exact ragged top-2048 + sparse MLA prefill over the paged fp8 cache and the fresh bf16 "
                                "rows), one layer", "queries": QN,
                    "keys": KN, "cached_prefix": KN - QN, "index_topk": K, "indexer_heads": 64,
                    "indexer_head_dim": 128, "mla_heads": H, "mla_dims": "576/512", "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": mq["TFLOPs"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": mq["fp8_mfma_frac"], "traffic": None, "kernel": "mqa_logits_kernel",
-                     "flops_per_launch": flops, "avg_launch_us": mq["us"]},
+        # the whole fused entry (every phase) priced as the logits contraction: a
+        # lower bound on its dominant kernel's rate
+        "roofline": {"bound": "mfma", "achieved": ft["TFLOPs"], "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": ft["fp8_mfma_frac"], "traffic": None,
+                     "kernel": "dsa_mqa_topk (mqa_logits_kernel<filter> + sample, threshold, list select)",
+                     "flops_per_launch": flops, "avg_launch_us": ft["us"]},
         "stages": out, "cpu_baseline": base,
     }
     if parity is not None:
         line["parity"] = parity
+    else:
+        line["parity"] = {"ok": fused_equal}
+    line["parity"]["fused_topk_equals_two_step_all_rows"] = fused_equal
+    line["parity"]["ok"] = bool(line["parity"]["ok"] and fused_equal)
+    parity = line["parity"]
     print(json.dumps(line), flush=True)
-    if parity is not None and not parity["ok"]:
+    if not parity["ok"]:
         print(f"parity FAILED: {parity}", file=sys.stderr)
         sys.exit(1)
 

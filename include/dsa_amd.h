@@ -328,6 +328,24 @@ DSA_API int dsa_mqa_logits(const uint8_t* q, const uint8_t* kv, const float* kv_
                            float* logits, int64_t logits_stride, int64_t num_cols,
                            int clean_logits, void* stream);
 
+/* Ragged fp8 MQA logits fused with the exact ragged top-2048 (prefill
+ * indexer): the result of dsa_mqa_logits followed by dsa_topk_transform_ragged
+ * (row_starts = offsets = ks, seq_lens = ke - ks clamped to [0, max_len]),
+ * bit for bit, without storing the logits.
+ *   q, kv, kv_scale, weights, ks, ke as for dsa_mqa_logits (num_heads 64)
+ *   max_len    >= every ke[i] - ks[i] that should count, <= dsa_topk_max_len()
+ *   out        [num_rows, 2048] int32: global key indices ks[i] + position, -1 padded
+ *   workspace  dsa_mqa_topk_workspace_bytes(num_rows, num_keys, 2048) bytes, 256-byte aligned
+ * Rows whose sampled threshold misses are redone from full logits in a second
+ * phase; the call reads one 4-byte counter back to the host (a stream sync).
+ * Replaces deep_gemm.fp8_mqa_logits + top_k_per_row_prefill at
+ * dlengine/runtime/layers/backends/dsa/indexer/lightning.py:1212-1246. */
+DSA_API size_t dsa_mqa_topk_workspace_bytes(int num_rows, int64_t num_keys, int top_k);
+DSA_API int dsa_mqa_topk(const uint8_t* q, const uint8_t* kv, const float* kv_scale, const float* weights,
+                         int64_t weights_stride, const int32_t* ks, const int32_t* ke, int num_rows,
+                         int64_t num_keys, int num_heads, int64_t max_len, int top_k, int32_t* out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 
 /* Paged indexer cache -> contiguous ragged keys and scales (prefill indexer).
  *   cache        [pages, page_bytes] uint8, page = [page_size x 128 fp8][page_size x f32]

@@ -45,6 +45,9 @@ SIGNATURES = {
                                        _P, _P]),
     "dsa_mqa_logits": (c_int, [_P, _P, _P, _P, c_int64, _P, _P, c_int, c_int64, c_int, _P, c_int64, c_int64, c_int,
                                _P]),
+    "dsa_mqa_topk_workspace_bytes": (c_size_t, [c_int, c_int64, c_int]),
+    "dsa_mqa_topk": (c_int, [_P, _P, _P, _P, c_int64, _P, _P, c_int, c_int64, c_int, c_int64, c_int, _P, _P, c_size_t,
+                             _P]),
     "dsa_sparse_mla_prefill": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int64, c_int, c_int, c_int,
                                        c_float, _P, _P, _P, _P]),
     "dsa_gather_indexer_cache": (c_int, [_P, c_int64, c_int, c_int, _P, c_int64, _P, c_int, c_int, c_int64, _P, _P,

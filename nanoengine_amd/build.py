@@ -15,7 +15,8 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libdsa_amd.so"
 SOURCES = ["capi.hip", "topk.hip", "indexer.hip", "sparse_mla.hip", "cache_store.hip",
-           "indexer_prologue.hip", "prefill_logits.hip", "sparse_mla_prefill.hip"]
+           "indexer_prologue.hip", "prefill_logits.hip", "sparse_mla_prefill.hip",
+           "prefill_topk.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -43,6 +44,7 @@ PER_FILE_FLAGS = {
     "sparse_mla_prefill.hip": [],
     "indexer_prologue.hip": [],
     "prefill_logits.hip": VGPR_FORM,
+    "prefill_topk.hip": VGPR_FORM,
 }
 
 

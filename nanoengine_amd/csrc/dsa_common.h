@@ -109,22 +109,36 @@ struct RowWs {
 
 // What the list select needs to redo a row whose list is unusable: the
 // indexer inputs of the row (query [rows, 64, 128] fp8, head weights
-// [rows, 64], the paged key cache) and a logits row to write.
+// [rows, 64], the paged key cache) and a logits row to write. With q NULL the
+// row is not redone in the kernel: its index is appended to defer_rows
+// (count in *defer_count) and its output is left for the caller to write.
 struct RowRepair {
   const uint8_t* q;
   const uint8_t* kv;
   const float* weights;
   float* logits;
   int64_t logits_stride;
+  int32_t* defer_rows;
+  uint32_t* defer_count;
 };
 
 // Launcher of the list select of the fused indexer + top-k entry point
 // (topk.hip): the exact top-k of each row's candidate list, with the page
 // translation; a row whose list is unusable is redone in place from its
 // full logits.
+// Without a page table, row b's positions are written plus offsets[b] (NULL: 0).
 int launch_list_select(const RowRepair& rp, const int32_t* seq_lens, int64_t max_len, RowWs* ws,
                        const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
-                       int32_t* out_page, int32_t* out_raw, int top_k, int rows, hipStream_t stream);
+                       const int32_t* offsets, int32_t* out_page, int32_t* out_raw, int top_k, int rows,
+                       hipStream_t stream);
+
+// The ragged fp8 MQA logits kernel (prefill_logits.hip). filter = false:
+// logits[i, j] for j in [ks[i], ke[i]). filter = true: nothing is stored;
+// key j of row i joins ws[i]'s candidate list (position j - ks[i]) when its
+// order key is at least ws[i].t_key.
+int launch_mqa_logits(bool filter, const uint8_t* q, const uint8_t* kv, const float* kv_scale, const float* weights,
+                      int64_t weights_stride, const int32_t* ks, const int32_t* ke, int num_rows, int64_t num_keys,
+                      float* logits, int64_t logits_stride, RowWs* ws, hipStream_t st);
 
 // Sparse MLA decode over physical slots of the paged fp8 cache (the body of
 // dsa_sparse_mla_decode). max_out (splits == 1 only) receives each head's

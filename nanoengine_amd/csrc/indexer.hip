@@ -699,9 +699,9 @@ extern "C" int dsa_indexer_topk(const uint8_t* q_fp8, const uint8_t* kv_cache, c
   mark(2);
   // 4. exact top-k of each row's list (with the page translation); a row
   // whose list is unusable is redone by its workgroup from its full logits
-  const RowRepair rp{q_fp8, kv_cache, weights, f.logits, f.logits_stride};
+  const RowRepair rp{q_fp8, kv_cache, weights, f.logits, f.logits_stride, nullptr, nullptr};
   const int rc = launch_list_select(rp, context_lens, max_context_len, f.ws, block_tables, block_table_stride, next_n,
-                                    6u, out_physical, out_logical, top_k, rows, st);
+                                    6u, nullptr, out_physical, out_logical, top_k, rows, st);
   mark(3);
   mark(4);
   return rc;

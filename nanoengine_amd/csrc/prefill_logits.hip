@@ -27,6 +27,7 @@
 // chunk c placed on XCD c % 8 (workgroups are dealt to the 8 XCDs round
 // robin), so the workgroups sharing a chunk's keys share one L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "dsa_common.h"
 #include "../../include/dsa_amd.h"
@@ -48,6 +49,14 @@ constexpr int kPfHeads = 64;
 struct PfLds {
   uint8_t key[kPfBufs][kPfStageBytes];
   float scale[kPfBufs][kPfStageKeys];
+};
+// The filter mode's per-wave candidate stage: (order key, position in the
+// row's window) of the keys at or above the row's threshold, moved to the
+// row's list in RowWs with one global atomic per flush.
+constexpr int kPfStageCap = 832;  // fills the LDS left by the key stages (157 KB of 160 KB)
+struct PfLdsFilter : PfLds {
+  uint32_t st_key[kPfWaves][kPfStageCap];
+  uint32_t st_pos[kPfWaves][kPfStageCap];
 };
 
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
@@ -100,20 +109,25 @@ __device__ __forceinline__ void issue_stage(PfLds* lds, int buf, int64_t kb, int
   if ((lane >> 3) == (wave & 7)) dma4(kv_scale + sk, lds_addr(&lds->scale[buf][64 * half]));
 }
 
-template <bool kPaged>
+// kFilter: no logits are stored; a key whose order key is at or above the
+// row's threshold (ws[row].t_key) joins the row's candidate list instead.
+template <bool kFilter>
 __global__ void __launch_bounds__(kPfThreads)
 mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv, const float* __restrict__ kv_scale,
                   const float* __restrict__ weights, int64_t w_stride, const int32_t* __restrict__ ks,
                   const int32_t* __restrict__ ke, int M, int64_t n_keys, int token_blocks, int64_t chunk_keys,
-                  float* __restrict__ logits, int64_t logits_stride) {
-  __shared__ PfLds lds;
+                  float* __restrict__ logits, int64_t logits_stride, RowWs* __restrict__ ws) {
+  __shared__ typename std::conditional<kFilter, PfLdsFilter, PfLds>::type lds;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // workgroup -> (token block, chunk): XCD b % 8 takes chunks c with c % 8 == b % 8
+  // (one chunk covers every key: workgroup b takes token block b; any
+  // workgroup past the last token block exits)
   const int b = blockIdx.x;
+  const bool one_chunk = chunk_keys >= n_keys;
   const int r = b >> 3;
-  const int tb = r % token_blocks;
-  const int chunk = (r / token_blocks) * 8 + (b & 7);
+  const int tb = one_chunk ? b : r % token_blocks;
+  const int chunk = one_chunk ? 0 : (r / token_blocks) * 8 + (b & 7);
   const int r0 = tb * kPfTokens;
   // key range of the block's 16 rows, intersected with the chunk
   int lo_i = INT32_MAX, hi_i = INT32_MIN;
@@ -154,6 +168,24 @@ mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
       for (int r = 0; r < 16; ++r) w[ht][r] = wb[ht * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
     }
   }
+  uint32_t tk = 0;
+  int cnt = 0;  // staged candidates of this wave's row (wave-uniform)
+  if constexpr (kFilter) tk = row_ok ? ws[rc].t_key : 0u;
+  auto flush = [&]() {
+    if constexpr (kFilter) {
+      if (cnt == 0) return;
+      RowWs& rw = ws[rc];
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&rw.count, (uint32_t)cnt);
+      base = __builtin_amdgcn_readfirstlane(base);
+      for (int e = lane; e < cnt; e += 64)
+        if (base + (uint32_t)e < (uint32_t)kListCap) {
+          rw.key[base + e] = lds.st_key[wave][e];
+          rw.pos[base + e] = lds.st_pos[wave][e];
+        }
+      cnt = 0;
+    }
+  };
   issue_stage(&lds, 0, lo, n_keys, kv, kv_scale, wave, lane);
   if (nstages > 1) issue_stage(&lds, 1, lo + kPfStageKeys, n_keys, kv, kv_scale, wave, lane);
   // the query loads above are ordinary loads: make the compiler's count start from zero
@@ -199,11 +231,27 @@ mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
       const float v = (hi32 ? part[1] : part[0]) + __shfl_xor(hi32 ? part[0] : part[1], 32, 64);
       const float sc = lds.scale[buf][64 * g + lane];
       const int64_t key = kb + 64 * g + lane;
-      if (key >= rks && key < rke && key < hi)
-        __builtin_nontemporal_store(v * sc, logits + (int64_t)row * logits_stride + key);
+      if constexpr (kFilter) {
+        const uint32_t okey = order_key(v * sc);
+        const bool pred = row_ok && key >= rks && key < rke && key < hi && okey >= tk;
+        const uint64_t m = __ballot(pred);
+        if (m) {
+          if (pred) {
+            const int slot = cnt + (int)__popcll(m & ((1ull << lane) - 1ull));
+            lds.st_key[wave][slot] = okey;
+            lds.st_pos[wave][slot] = (uint32_t)(key - rks);
+          }
+          cnt += (int)__popcll(m);
+          if (cnt > kPfStageCap - 64) flush();
+        }
+      } else {
+        if (key >= rks && key < rke && key < hi)
+          __builtin_nontemporal_store(v * sc, logits + (int64_t)row * logits_stride + key);
+      }
     }
     if (s + 2 < nstages) issue_stage(&lds, (s + 2) % kPfBufs, kb + 2 * kPfStageKeys, n_keys, kv, kv_scale, wave, lane);
   }
+  flush();
 }
 
 // logits[i, j] = -inf for j outside [ks[i], ke[i]), j < n_cols.
@@ -276,6 +324,37 @@ prefill_windows_kernel(const void* __restrict__ cu_q, const void* __restrict__ c
 }
 
 }  // namespace
+
+// Both modes of the logits kernel on one grid: token blocks x key chunks.
+int launch_mqa_logits(bool filter, const uint8_t* q, const uint8_t* kv, const float* kv_scale, const float* weights,
+                      int64_t weights_stride, const int32_t* ks, const int32_t* ke, int num_rows, int64_t num_keys,
+                      float* logits, int64_t logits_stride, RowWs* ws, hipStream_t st) {
+  const int token_blocks = (num_rows + kPfTokens - 1) / kPfTokens;
+  int64_t chunks, chunk_keys;
+  if (token_blocks >= 512 && num_keys <= 32 * kPfStageKeys) {
+    // few keys, many rows: one chunk, so that each query block is read once
+    chunks = 1;
+    chunk_keys = std::max<int64_t>(num_keys, 1);
+  } else {
+    // chunks: a multiple of 8 (one XCD each), enough workgroups for the 256 CUs
+    chunks = 8;
+    while ((int64_t)token_blocks * chunks < 1024 && chunks * 64 * 8 <= num_keys) chunks *= 2;
+    chunk_keys = (num_keys + chunks - 1) / chunks;
+    chunk_keys = (chunk_keys + kPfStageKeys - 1) / kPfStageKeys * kPfStageKeys;
+  }
+  const int64_t grid = (int64_t)token_blocks * chunks;
+  if (grid > INT32_MAX) return set_error(kInvalidArgument, "mqa logits: grid too large");
+  if (filter)
+    hipLaunchKernelGGL(mqa_logits_kernel<true>, dim3((unsigned)grid), dim3(kPfThreads), 0, st, q, kv, kv_scale,
+                       weights, weights_stride, ks, ke, num_rows, num_keys, token_blocks, chunk_keys, logits,
+                       logits_stride, ws);
+  else
+    hipLaunchKernelGGL(mqa_logits_kernel<false>, dim3((unsigned)grid), dim3(kPfThreads), 0, st, q, kv, kv_scale,
+                       weights, weights_stride, ks, ke, num_rows, num_keys, token_blocks, chunk_keys, logits,
+                       logits_stride, ws);
+  return check_launch(filter ? "mqa logits (filter)" : "dsa_mqa_logits");
+}
+
 }  // namespace dsa
 
 extern "C" {
@@ -302,18 +381,8 @@ int dsa_mqa_logits(const uint8_t* q, const uint8_t* kv, const float* kv_scale, c
     if (int rc = check_launch("dsa_mqa_logits (clean)")) return rc;
   }
   if (num_keys == 0) return kOk;
-  const int token_blocks = (num_rows + kPfTokens - 1) / kPfTokens;
-  // chunks: a multiple of 8 (one XCD each), enough workgroups for the 256 CUs
-  int64_t chunks = 8;
-  while ((int64_t)token_blocks * chunks < 1024 && chunks * 64 * 8 <= num_keys) chunks *= 2;
-  int64_t chunk_keys = (num_keys + chunks - 1) / chunks;
-  chunk_keys = (chunk_keys + kPfStageKeys - 1) / kPfStageKeys * kPfStageKeys;
-  const int64_t grid = (int64_t)token_blocks * chunks;
-  if (grid > INT32_MAX) return set_error(kInvalidArgument, "dsa_mqa_logits: grid too large");
-  hipLaunchKernelGGL(mqa_logits_kernel<false>, dim3((unsigned)grid), dim3(kPfThreads), 0, st, q, kv, kv_scale,
-                     weights, weights_stride, ks, ke, num_rows, num_keys, token_blocks, chunk_keys, logits,
-                     logits_stride);
-  return check_launch("dsa_mqa_logits");
+  return launch_mqa_logits(false, q, kv, kv_scale, weights, weights_stride, ks, ke, num_rows, num_keys, logits,
+                           logits_stride, nullptr, st);
 }
 
 int dsa_prefill_windows(const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64, int num_seqs,

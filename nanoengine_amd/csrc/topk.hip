@@ -64,6 +64,20 @@ struct TopkSmem {
 };
 constexpr size_t kTopkSmemBytes = sizeof(TopkSmem);
 
+// LDS of the list select: the candidates of a level's threshold bin are kept
+// as 16-bit indices into the row's list (values re-read from global), so two
+// workgroups fit on a CU. A row the kernel repairs itself uses TopkSmem.
+struct ListSmem {
+  uint32_t hist[kHistBins];
+  uint32_t bitmap[kBitmapWords];
+  uint16_t list[2][kListCap];
+  uint32_t wave_sum[16];
+  uint32_t list_count[2];
+  uint32_t tb, above, eq;
+};
+static_assert(kListCap <= 65536, "list indices are 16-bit");
+static_assert(sizeof(ListSmem) <= sizeof(TopkSmem), "a repairing launch covers the list layout");
+
 __device__ __forceinline__ uint32_t radix_digit(int level, uint32_t key, uint32_t pos) {
   switch (level) {
     case 0: return key >> 20;
@@ -807,12 +821,17 @@ __device__ void repair_row_logits(const RowRepair& rp, const int32_t* __restrict
   }
 }
 
-__global__ void __launch_bounds__(kTopkThreads)
-topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* __restrict__ ws,
-                 const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
-                 int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k, const RowRepair rp) {
+// The list select of one row per workgroup. kRepair: a row whose list is
+// unusable is redone in the kernel from its full logits (rp.q set, the launch
+// reserves TopkSmem); otherwise it is appended to rp.defer_rows.
+template <bool kRepair>
+__device__ __forceinline__ void list_select_row(const int32_t* __restrict__ seq_lens, int64_t max_len,
+                                                RowWs* __restrict__ ws, const int32_t* __restrict__ page_table,
+                                                int64_t pt_stride, int pt_div, uint32_t page_bits,
+                                                const int32_t* __restrict__ offsets, int32_t* __restrict__ out_page,
+                                                int32_t* __restrict__ out_raw, int top_k, const RowRepair& rp) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
-  TopkSmem& s = *reinterpret_cast<TopkSmem*>(smem_raw);
+  ListSmem& s = *reinterpret_cast<ListSmem*>(smem_raw);
   constexpr int NT = kTopkThreads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.x;
@@ -825,7 +844,7 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
   out.raw = out_raw ? out_raw + (int64_t)b * top_k : nullptr;
   out.pt = page_table ? page_table + (int64_t)(b / pt_div) * pt_stride : nullptr;
   out.page_bits = page_bits;
-  out.offset = 0;
+  out.offset = (!page_table && offsets) ? offsets[b] : 0;
 
   if (len <= top_k) {
     for (int i = tid; i < top_k; i += NT) out.emit(i, i < len ? i : -1);
@@ -834,12 +853,19 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
   const uint32_t cand = w.count;
   if (cand < (uint32_t)top_k || cand > (uint32_t)kListCap) {
     // The sample misjudged this row's threshold: its list cannot give the
-    // exact top-k. Redo the row here, from its full logits.
+    // exact top-k. Redo the row here, from its full logits, or leave it to
+    // the caller.
     if (tid == 0) w.failed = 1u;
-    repair_row_logits(rp, page_table + (int64_t)(b / pt_div) * pt_stride, b, len);
-    __syncthreads();  // the row's logits (global) are visible to the whole workgroup
-    const RowIn in{rp.logits, rp.logits_stride, seq_lens, nullptr, max_len};
-    finish_row(s, in, nullptr, nullptr, page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k, b);
+    if constexpr (kRepair) {
+      repair_row_logits(rp, page_table + (int64_t)(b / pt_div) * pt_stride, b, len);
+      __syncthreads();  // the row's logits (global) are visible to the whole workgroup
+      const RowIn in{rp.logits, rp.logits_stride, seq_lens, nullptr, max_len};
+      // a repairing launch reserves the full select's LDS
+      finish_row(*reinterpret_cast<TopkSmem*>(smem_raw), in, nullptr, nullptr, page_table, pt_stride, pt_div,
+                 page_bits, out_page, out_raw, top_k, b);
+    } else {
+      if (tid == 0) rp.defer_rows[atomicAdd(rp.defer_count, 1u)] = b;
+    }
     return;
   }
   const uint32_t t_key = w.t_key;
@@ -931,8 +957,7 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
         mark(cl[u]);
       } else if (!last && d == tb) {
         const uint32_t slot = atomicAdd(&s.list_count[0], 1u);
-        s.list_key[0][slot] = ch[u];
-        s.list_pos[0][slot] = cl[u];
+        s.list[0][slot] = (uint16_t)(u * NT + tid);
       }
     }
     __syncthreads();
@@ -951,22 +976,23 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
     for (int i = tid; i < nbins; i += NT) s.hist[i] = 0u;
     if (tid == 0) s.list_count[nxt] = 0u;
     __syncthreads();
-    for (uint32_t e = tid; e < n; e += NT)
-      atomicAdd(&s.hist[digit(composite(s.list_key[cur][e], s.list_pos[cur][e]), L)], 1u);
+    // the threshold bin's candidates, re-read from the row's list (L2)
+    auto cand_h = [&](uint32_t i) { return w.key[s.list[cur][i]] - t_key; };
+    auto cand_p = [&](uint32_t i) { return kIdxMax - w.pos[s.list[cur][i]]; };
+    for (uint32_t e = tid; e < n; e += NT) atomicAdd(&s.hist[digit(composite(cand_h(e), cand_p(e)), L)], 1u);
     __syncthreads();
     find_threshold<NT>(s.hist, s.wave_sum, nbins, remain, &s.tb, &s.above, &s.eq);
     const uint32_t tb = s.tb, above = s.above, eq = s.eq;
     remain -= above;
     last = (eq == remain) || L == nlev - 1;
     for (uint32_t e = tid; e < n; e += NT) {
-      const uint32_t h = s.list_key[cur][e], p = s.list_pos[cur][e];
+      const uint32_t h = cand_h(e), p = cand_p(e);
       const uint32_t d = digit(composite(h, p), L);
       if (d > tb || (last && d == tb)) {
         mark(p);
       } else if (!last && d == tb) {
         const uint32_t slot = atomicAdd(&s.list_count[nxt], 1u);
-        s.list_key[nxt][slot] = h;
-        s.list_pos[nxt][slot] = p;
+        s.list[nxt][slot] = s.list[cur][e];
       }
     }
     __syncthreads();
@@ -1004,6 +1030,24 @@ topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* _
   }
 }
 
+__global__ void __launch_bounds__(kTopkThreads)
+topk_list_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* __restrict__ ws,
+                 const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                 int32_t* __restrict__ out_page, int32_t* __restrict__ out_raw, int top_k, const RowRepair rp) {
+  list_select_row<true>(seq_lens, max_len, ws, page_table, pt_stride, pt_div, page_bits, nullptr, out_page, out_raw,
+                        top_k, rp);
+}
+
+// Four waves per SIMD (<= 128 VGPRs): with the list layout, two workgroups per CU.
+__global__ void __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(4)))
+topk_list_defer_kernel(const int32_t* __restrict__ seq_lens, int64_t max_len, RowWs* __restrict__ ws,
+                       const int32_t* __restrict__ page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
+                       const int32_t* __restrict__ offsets, int32_t* __restrict__ out_page,
+                       int32_t* __restrict__ out_raw, int top_k, const RowRepair rp) {
+  list_select_row<false>(seq_lens, max_len, ws, page_table, pt_stride, pt_div, page_bits, offsets, out_page, out_raw,
+                         top_k, rp);
+}
+
 __global__ void topk_to_physical_kernel(const int32_t* __restrict__ topk, int64_t topk_stride,
                                         const int32_t* __restrict__ bt, int64_t bt_stride,
                                         int table_width, int rows, int k, int rows_per_table,
@@ -1034,6 +1078,9 @@ static int prepare_topk_kernel() {
     if (e == hipSuccess)
       e = hipFuncSetAttribute((const void*)topk_list_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)kTopkSmemBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)topk_list_defer_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)sizeof(ListSmem));
     status = e == hipSuccess ? 0 : 1;
     if (status) return set_error(kLaunchFailed, "topk: cannot reserve %zu B of LDS: %s",
                                  kTopkSmemBytes, hipGetErrorString(e));
@@ -1105,10 +1152,15 @@ static int launch_topk(const RowIn& in, int batch, const int32_t* offsets, const
 
 int launch_list_select(const RowRepair& rp, const int32_t* seq_lens, int64_t max_len, RowWs* ws,
                        const int32_t* page_table, int64_t pt_stride, int pt_div, uint32_t page_bits,
-                       int32_t* out_page, int32_t* out_raw, int top_k, int rows, hipStream_t stream) {
+                       const int32_t* offsets, int32_t* out_page, int32_t* out_raw, int top_k, int rows,
+                       hipStream_t stream) {
   if (int rc = prepare_topk_kernel()) return rc;
-  hipLaunchKernelGGL(topk_list_kernel, dim3(rows), dim3(kTopkThreads), kTopkSmemBytes, stream, seq_lens, max_len, ws,
-                     page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k, rp);
+  if (rp.q)
+    hipLaunchKernelGGL(topk_list_kernel, dim3(rows), dim3(kTopkThreads), kTopkSmemBytes, stream, seq_lens, max_len,
+                       ws, page_table, pt_stride, pt_div, page_bits, out_page, out_raw, top_k, rp);
+  else
+    hipLaunchKernelGGL(topk_list_defer_kernel, dim3(rows), dim3(kTopkThreads), sizeof(ListSmem), stream, seq_lens,
+                       max_len, ws, page_table, pt_stride, pt_div, page_bits, offsets, out_page, out_raw, top_k, rp);
   return check_launch("dsa_indexer_topk(select)");
 }
 

@@ -193,8 +193,9 @@ def compute_prefill_topk_paged(q_fp8: torch.Tensor, weights: torch.Tensor, cu_se
     The windows and the batch checks run in one kernel (``ops.prefill_windows``);
     the host reads its 32-byte status once, which is the call's only
     synchronisation. The paged keys are gathered to ragged order once, then
-    the logits go chunk by chunk through one reused workspace, each chunk
-    followed by its top-k (the fused exact select for 2048).
+    for top-2048 the logits kernel feeds the exact select directly
+    (``ops.mqa_topk``: no logits buffer); for other k the logits go chunk by
+    chunk through one reused buffer, each chunk followed by its top-k.
     """
     if query_chunk is not None and query_chunk <= 0:
         raise ValueError(f"query_chunk must be positive, got {query_chunk}")
@@ -234,6 +235,16 @@ def compute_prefill_topk_paged(q_fp8: torch.Tensor, weights: torch.Tensor, cu_se
     keys = key_bytes.view(torch.float8_e4m3fn)
     key_scales = scale_bytes.view(torch.float32).reshape(-1)
 
+    if index_topk == 2048 and PREFILL_FUSED_TOPK:
+        # logits and top-k in one pass: no [rows, total_k] logits buffer
+        rows = min(query_chunk or num_queries, num_queries)
+        workspace = torch.empty(ops.mqa_topk_workspace_bytes(rows, total_k), dtype=torch.uint8, device=dev)
+        for r0 in range(0, num_queries, rows):
+            r1 = min(r0 + rows, num_queries)
+            ops.mqa_topk(q_fp8[r0:r1], keys, key_scales, weights[r0:r1], ks[r0:r1], ke[r0:r1], max_seqlen_k,
+                         indices[r0:r1], index_topk, workspace=workspace)
+        return indices
+
     fused = index_topk == 2048
     rows = _prefill_chunk_rows(num_queries, total_k, dev, query_chunk)
     workspace = torch.empty(rows, total_k, dtype=torch.float32, device=dev)
@@ -249,6 +260,11 @@ def compute_prefill_topk_paged(q_fp8: torch.Tensor, weights: torch.Tensor, cu_se
         else:
             _select_rows_descending(logits, indices[r0:r1], index_topk)
     return indices
+
+
+# top-2048 through ops.mqa_topk (logits never stored); False scores each chunk
+# of rows into a logits buffer and selects with the ragged top-k
+PREFILL_FUSED_TOPK = True
 
 
 def _score_chunk(q, keys, key_scales, weights, ks, ke, out, clean: bool) -> None:

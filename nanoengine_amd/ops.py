@@ -487,6 +487,42 @@ def mqa_logits(q_fp8: torch.Tensor, kv_fp8: torch.Tensor, kv_scale: torch.Tensor
               out.data_ptr(), out.stride(0), out.shape[1], int(bool(clean_logits)), _stream(dev))
 
 
+def mqa_topk_workspace_bytes(num_rows: int, num_keys: int, top_k: int = 2048) -> int:
+    return int(_lib.load().dsa_mqa_topk_workspace_bytes(int(num_rows), int(num_keys), int(top_k)))
+
+
+def mqa_topk(q_fp8: torch.Tensor, kv_fp8: torch.Tensor, kv_scale: torch.Tensor, weights: torch.Tensor,
+             ks: torch.Tensor, ke: torch.Tensor, max_len: int, out: torch.Tensor, top_k: int = 2048,
+             workspace: torch.Tensor | None = None) -> None:
+    """Ragged fp8 MQA logits + exact top-2048 without a logits buffer: out
+    [M, 2048] int32 global key indices, -1 padded (see dsa_mqa_topk)."""
+    if top_k != 2048:
+        raise ValueError(f"ragged Indexer top_k must be 2048, got {top_k}")
+    _require(q_fp8.dim() == 3 and q_fp8.shape[1] == INDEXER_HEADS and q_fp8.shape[2] == INDEXER_HEAD_DIM
+             and q_fp8.is_contiguous(), "q must be contiguous fp8 [M, 64, 128]", ValueError)
+    m = q_fp8.shape[0]
+    kv2 = kv_fp8.reshape(-1, INDEXER_HEAD_DIM)
+    _require(kv2.is_contiguous(), "kv must be contiguous fp8 [N, 128]", ValueError)
+    n = kv2.shape[0]
+    sc = kv_scale.reshape(-1)
+    _require(sc.numel() == n and sc.dtype == torch.float32 and sc.is_contiguous(),
+             "kv scales must be contiguous f32 [N]", ValueError)
+    _require(weights.shape == (m, INDEXER_HEADS) and weights.dtype == torch.float32 and weights.stride(1) == 1,
+             "weights must be f32 [M, 64]", ValueError)
+    for t in (ks, ke):
+        _require(t.dim() == 1 and t.shape[0] == m and t.dtype == torch.int32 and t.is_contiguous(),
+                 "k start/end must be contiguous int32 [M]", ValueError)
+    _require(out.dtype == torch.int32 and tuple(out.shape) == (m, top_k) and out.is_contiguous(),
+             "out must be contiguous int32 [M, 2048]", ValueError)
+    dev = _check_cuda(q_fp8, kv2, sc, weights, ks, ke, out)
+    need = mqa_topk_workspace_bytes(m, n, top_k)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    _lib.call("dsa_mqa_topk", _as_bytes(q_fp8).data_ptr(), _as_bytes(kv2).data_ptr(), sc.data_ptr(),
+              weights.data_ptr(), weights.stride(0), ks.data_ptr(), ke.data_ptr(), m, n, INDEXER_HEADS,
+              int(max_len), int(top_k), out.data_ptr(), *_ws_args(workspace), _stream(dev))
+
+
 def mla_prefill_kv(k_cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_q: torch.Tensor,
                    cu_seqlens_k: torch.Tensor, fresh: torch.Tensor, total_k: int, out: torch.Tensor) -> None:
     """Ragged bf16 keys [total_k, 576] of a prefill chunk: cached rows restored

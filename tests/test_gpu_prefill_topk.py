@@ -141,8 +141,8 @@ def test_prefill_windows_match_oracle(cuda, dtype):
 
 
 def test_driver_long_rows_fused_topk_is_exact(cuda, monkeypatch):
-    """top_k = 2048 over 65537- and 65538-key windows goes through the fused
-    ragged select (clean_logits=False), which is exact against torch.topk."""
+    """top_k = 2048 over 65537- and 65538-key windows, with the logits-buffer
+    path: the ragged select (clean_logits=False) is exact against torch.topk."""
     print("prefill driver long rows", flush=True)
     seen = []
 
@@ -153,6 +153,7 @@ def test_driver_long_rows_fused_topk_is_exact(cuda, monkeypatch):
         seen.append(out.clone())
 
     monkeypatch.setattr(indexer_module, "_score_chunk", fake_logits)
+    monkeypatch.setattr(indexer_module, "PREFILL_FUSED_TOPK", False)
     cache = torch.zeros(1, 64 * 132, dtype=torch.uint8, device=cuda)
     q = torch.zeros(2, 64, 128, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)
     w = torch.ones(2, 64, dtype=torch.float32, device=cuda)
