@@ -25,7 +25,16 @@
 //
 // Grid: token blocks x key chunks, with the chunk count a multiple of 8 and
 // chunk c placed on XCD c % 8 (workgroups are dealt to the 8 XCDs round
-// robin), so the workgroups sharing a chunk's keys share one L2.
+// robin), so the workgroups sharing a chunk's keys share one L2; a short key
+// set with many query blocks runs as one chunk (each query block read once).
+//
+// Filter mode (the fused top-k of prefill_topk.hip): instead of storing the
+// logit, each wave compares the order key of its 64 logits with its row's
+// threshold, appends the passing (key, position) pairs to a per-wave LDS
+// stage (ballot + popcount slots) and moves the stage to the row's global
+// list with one atomic when it could overflow and at the end. The stage is
+// sized so that a typical chunk flushes once, at the end: a flush waits for
+// the atomic's return, which also drains the wave's key prefetches.
 #include <algorithm>
 #include <type_traits>
 
