@@ -134,6 +134,50 @@ __device__ uint32_t block_exclusive_scan(uint32_t* wave_sum, uint32_t x, uint32_
   return before + v - x;
 }
 
+// Positions of the set bits of bitmap[0, nwords) in ascending order into
+// sel[0, top_k) (*total = all set bits). Thread t owns the 16-byte-aligned
+// word range [4 q t, 4 q (t + 1)), q = ceil(nwords / 4NT), read with 16-byte
+// loads (lanes 4q words apart: at most 2-way bank conflicts, where single
+// words would conflict q-ways) and kept in registers for the second pass;
+// words at or past nwords count as zero. Ends with a barrier.
+template <int NT>
+__device__ void compact_bitmap(const uint32_t* bitmap, int nwords, uint32_t* wave_sum, uint32_t* sel, int top_k,
+                               uint32_t* total_out) {
+  constexpr int kMaxQ = kBitmapWords / (4 * NT);
+  static_assert(kMaxQ >= 1 && kBitmapWords % (4 * NT) == 0, "bitmap words per thread");
+  const int tid = threadIdx.x;
+  const int q = (nwords + 4 * NT - 1) / (4 * NT);
+  const int w0 = tid * 4 * q;
+  uint32_t v[4 * kMaxQ];
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxQ; ++i) {
+    uint4 x = {0u, 0u, 0u, 0u};
+    if (i < q && w0 + 4 * i < nwords) x = *reinterpret_cast<const uint4*>(bitmap + w0 + 4 * i);
+    v[4 * i] = x.x;
+    v[4 * i + 1] = w0 + 4 * i + 1 < nwords ? x.y : 0u;
+    v[4 * i + 2] = w0 + 4 * i + 2 < nwords ? x.z : 0u;
+    v[4 * i + 3] = w0 + 4 * i + 3 < nwords ? x.w : 0u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cnt += __popc(v[4 * i + k]);
+  }
+  uint32_t total = 0;
+  uint32_t at = block_exclusive_scan<NT>(wave_sum, cnt, &total);
+  __syncthreads();  // sel may alias buffers read before this call
+#pragma unroll
+  for (int k = 0; k < 4 * kMaxQ; ++k) {
+    uint32_t bits = v[k];
+    while (bits) {
+      const int bit = __ffs(bits) - 1;
+      bits &= bits - 1;
+      if (at < (uint32_t)top_k) sel[at] = (uint32_t)(((w0 + k) << 5) + bit);
+      ++at;
+    }
+  }
+  __syncthreads();
+  *total_out = total;
+}
+
 
 struct RowOut {
   int32_t* page;       // page-translated output (or the untranslated output)
@@ -427,26 +471,12 @@ __device__ void finish_row(TopkSmem& s, const RowIn& in, RowWs* __restrict__ ws,
     }
   }
 
-  // Compact the bitmap in position order: each thread owns a contiguous word range.
-  const int wpt = (nwords + kTopkThreads - 1) / kTopkThreads;
-  const int w_begin = min(tid * wpt, nwords), w_end = min(w_begin + wpt, nwords);
-  uint32_t cnt = 0;
-  for (int w = w_begin; w < w_end; ++w) cnt += __popc(s.bitmap[w]);
-  uint32_t total = 0;
-  uint32_t slot = block_exclusive_scan<kTopkThreads>(s.wave_sum, cnt, &total);
-  // positions in ascending order into LDS, then the page-table translation as
-  // independent loads spread over all threads
+  // Compact the bitmap in position order: positions in ascending order into
+  // LDS, then the page-table translation as independent loads spread over all
+  // threads
   uint32_t* sel = s.list_pos[0];
-  for (int w = w_begin; w < w_end; ++w) {
-    uint32_t bits = s.bitmap[w];
-    while (bits) {
-      const int bit = __ffs(bits) - 1;
-      bits &= bits - 1;
-      if (slot < (uint32_t)top_k) sel[slot] = (uint32_t)((w << 5) + bit);
-      ++slot;
-    }
-  }
-  __syncthreads();
+  uint32_t total = 0;
+  compact_bitmap<kTopkThreads>(s.bitmap, nwords, s.wave_sum, sel, top_k, &total);
   for (int i = tid; i < top_k; i += kTopkThreads) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
 }
 
@@ -759,24 +789,9 @@ topk_onepass_kernel(const RowIn in, const int32_t* __restrict__ offsets, const i
   }
 
   // ---- 4. compaction in position order (two words per thread) and output
-  const int wpt = (nwords + NT - 1) / NT;
-  const int w_begin = min(tid * wpt, nwords), w_end = min(w_begin + wpt, nwords);
-  uint32_t cnt = 0;
-  for (int w = w_begin; w < w_end; ++w) cnt += __popc(s.bitmap[w]);
-  uint32_t total = 0;
-  uint32_t at = block_exclusive_scan<NT>(s.wave_sum, cnt, &total);
   uint32_t* sel = s.list_pos[0];
-  __syncthreads();  // the list buffers are done with
-  for (int w = w_begin; w < w_end; ++w) {
-    uint32_t bits = s.bitmap[w];
-    while (bits) {
-      const int bit = __ffs(bits) - 1;
-      bits &= bits - 1;
-      if (at < (uint32_t)top_k) sel[at] = (uint32_t)((w << 5) + bit);
-      ++at;
-    }
-  }
-  __syncthreads();
+  uint32_t total = 0;
+  compact_bitmap<NT>(s.bitmap, nwords, s.wave_sum, sel, top_k, &total);
   for (int i = tid; i < top_k; i += NT) out.emit(i, i < (int)total ? (int32_t)sel[i] : -1);
 }
 
@@ -1000,24 +1015,9 @@ __device__ __forceinline__ void list_select_row(const int32_t* __restrict__ seq_
   }
 
   // compaction in position order and output
-  const int wpt = (nwords + NT - 1) / NT;
-  const int w_begin = min(tid * wpt, nwords), w_end = min(w_begin + wpt, nwords);
-  uint32_t cnt = 0;
-  for (int wd = w_begin; wd < w_end; ++wd) cnt += __popc(s.bitmap[wd]);
-  uint32_t total = 0;
-  uint32_t at = block_exclusive_scan<NT>(s.wave_sum, cnt, &total);
   uint32_t* sel = s.hist;  // 4096 entries >= top_k
-  __syncthreads();
-  for (int wd = w_begin; wd < w_end; ++wd) {
-    uint32_t bits = s.bitmap[wd];
-    while (bits) {
-      const int bit = __ffs(bits) - 1;
-      bits &= bits - 1;
-      if (at < (uint32_t)top_k) sel[at] = (uint32_t)((wd << 5) + bit);
-      ++at;
-    }
-  }
-  __syncthreads();
+  uint32_t total = 0;
+  compact_bitmap<NT>(s.bitmap, nwords, s.wave_sum, sel, top_k, &total);
   if (pt_lds) {
     const uint32_t mask = (1u << page_bits) - 1u;
     for (int i = tid; i < top_k; i += NT) {
