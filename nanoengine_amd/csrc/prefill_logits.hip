@@ -226,12 +226,16 @@ mqa_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ kv,
         c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[1][1], kb1, c1, 0, 0, 0, 127, 0, 127);
         // c_ht[r]: head 32ht + 8(r/4) + 4(lane/32) + r%4, key kb + 32kt + lane%32
         float a0 = 0.f, a1 = 0.f;  // two chains: no fma waits on the previous one
+        // the epilogue issues ahead of the other waves' MFMAs (measured ~2-3% faster
+        // than equal priority; raising the MFMA sequence instead gains ~1%)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           a0 = fmaf(w[0][r], relu(c0[r]), a0);
           a1 = fmaf(w[1][r], relu(c1[r]), a1);
         }
         part[t] = a0 + a1;
+        __builtin_amdgcn_s_setprio(0);
       }
       // the two lane halves hold the two halves of the heads: lane l < 32
       // keeps the half's first key tile (key l), lane l >= 32 its second
