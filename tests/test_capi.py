@@ -115,3 +115,27 @@ def test_prefill_entry_points_reject_bad_arguments(lib):
     bad = list(args)
     bad[26] = P                                                             # no workspace
     assert lib.dsa_sparse_mla_prefill_paged(*bad, ws, P) == 1
+
+
+def test_fused_prefill_topk_rejects_bad_arguments(lib):
+    P = None
+    one = ctypes.c_void_p(16)  # a non-null, aligned address that is never dereferenced
+    rows, keys = 10, 5000
+    ws = lib.dsa_mqa_topk_workspace_bytes(rows, keys, 2048)
+    # the per-row candidate lists (6144 (key, position) pairs + 16-byte header) dominate
+    assert ws >= rows * (16 + 6144 * 8)
+    assert lib.dsa_mqa_topk_workspace_bytes(0, keys, 2048) == 0
+    assert lib.dsa_mqa_topk_workspace_bytes(2 * rows, keys, 2048) > ws
+    args = [one, one, one, one, 64, one, one, rows, keys, 64, keys, 2048, one, one]
+    assert lib.dsa_mqa_topk(*args, ws - 1, P) == 4                         # workspace too small
+    assert b"workspace" in lib.dsa_last_error()
+    bad = list(args); bad[11] = 512                                        # ragged top-k is 2048 only
+    assert lib.dsa_mqa_topk(*bad, ws, P) == 1
+    bad = list(args); bad[9] = 32                                          # 64 indexer heads
+    assert lib.dsa_mqa_topk(*bad, ws, P) == 2
+    bad = list(args); bad[10] = (1 << 18) + 1                              # rows past the select's limit
+    assert lib.dsa_mqa_topk(*bad, ws, P) == 2
+    bad = list(args); bad[0] = P                                           # no query
+    assert lib.dsa_mqa_topk(*bad, ws, P) == 1
+    bad = list(args); bad[7] = 0                                           # nothing to do
+    assert lib.dsa_mqa_topk(*bad, 0, P) == 0
