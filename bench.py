@@ -18,6 +18,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [
        python bench.py --copy-calib   (a plain 1 GiB device copy, for scaling
                                        rocprofv3 FETCH_SIZE/WRITE_SIZE)
        python bench.py --only {fused,indexer,topk,mla}   (profiling: one stage only)
+       python bench.py --micro        (the microbenchmarks behind the kernels' design)
 """
 from __future__ import annotations
 
@@ -51,6 +52,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample")
     p.add_argument("--copy-calib", action="store_true")
+    p.add_argument("--micro", action="store_true",
+                   help="run the microbenchmarks of libdsa_microbench.so (one JSON line each)")
     p.add_argument("--unfused", action="store_true", help="indexer logits + top-k as two operators")
     p.add_argument("--config", type=int, choices=[1, 2, 3, 4], default=2,
                    help="1: sparse MLA decode alone, B=32 x 32K; 2: decode B=128 x 64K (the headline); "
@@ -81,6 +84,100 @@ def copy_calib():
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": n, "launches": 5}))
+
+
+def micro():
+    """The measurements behind the kernels' design (nanoengine_amd/csrc/microbench.hip)."""
+    import ctypes
+
+    import torch
+
+    from nanoengine_amd.build import MICROBENCH_LIB
+
+    lib = ctypes.CDLL(str(MICROBENCH_LIB))
+    dev = torch.device("cuda:0")
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e-3)
+        return best
+
+    def check(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: HIP error {rc}")
+
+    g = torch.Generator(device=dev).manual_seed(1)
+    # 1. random 8448-byte pages, the config-2 indexer pool (131072 pages = 1.107 GB)
+    npages, grid = 131072, 512
+    pool = torch.randint(0, 255, (npages * 8448,), dtype=torch.uint8, device=dev, generator=g)
+    ids = torch.randperm(npages, device=dev, generator=g).to(torch.int32)
+    per_wave = npages // (grid * 4)
+    t = timed(lambda: check(lib.dsa_mb_page_read(ctypes.c_void_p(pool.data_ptr()), ctypes.c_void_p(ids.data_ptr()),
+                                                 per_wave, grid, ctypes.c_void_p(sink.data_ptr()), st), "page_read"))
+    nbytes = npages * 8448
+    print(json.dumps({"micro": "page_read", "pages": npages, "page_bytes": 8448, "waves": grid * 4,
+                      "us": round(t * 1e6, 1), "TBps": round(nbytes / t / 1e12, 3)}), flush=True)
+    del pool, ids
+    # 2. random 656-byte rows into LDS (5 GB pool, 64-row blocks, two in flight)
+    nrows, nblk, grid = (5 << 30) // 656, 32, 256
+    pool = torch.zeros(nrows * 656, dtype=torch.uint8, device=dev)
+    t = timed(lambda: check(lib.dsa_mb_row_gather(ctypes.c_void_p(pool.data_ptr()), ctypes.c_int64(nrows), nblk,
+                                                  grid, ctypes.c_void_p(sink.data_ptr()), st), "row_gather"))
+    nbytes = grid * nblk * 64 * 656
+    print(json.dumps({"micro": "row_gather_lds", "rows": grid * nblk * 64, "row_bytes": 656,
+                      "workgroups": grid, "us": round(t * 1e6, 1), "TBps": round(nbytes / t / 1e12, 3)}), flush=True)
+    del pool
+    # 3. LDS read bandwidth per CU (clock64 cycles of each workgroup)
+    cyc = torch.zeros(256 * 16, dtype=torch.int64, device=dev)
+    iters = 4096
+    for waves in (4, 8, 16):
+        check(lib.dsa_mb_lds_read(waves, iters, 256, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(cyc.data_ptr()),
+                                  st), "lds_read")
+        torch.cuda.synchronize()
+        c = float(cyc[:256].double().mean())
+        print(json.dumps({"micro": "lds_read_b128", "waves_per_cu": waves,
+                          "bytes_per_clk_per_cu": round(iters * 8 * 16 * 64 * waves / c, 1)}), flush=True)
+    # 4. VALU issue: cycles per independent instruction of one wave
+    for op, name in ((0, "v_fma_f32"), (1, "v_exp_f32")):
+        for threads in (256, 512, 1024):
+            iters = 2048
+            check(lib.dsa_mb_valu_issue(op, threads, iters, 256, ctypes.c_void_p(sink.data_ptr()),
+                                        ctypes.c_void_p(cyc.data_ptr()), st), "valu_issue")
+            torch.cuda.synchronize()
+            c = float(cyc[:256 * threads // 64].double().mean())
+            print(json.dumps({"micro": "valu_issue", "op": name, "waves_per_simd": threads // 256,
+                              "cycles_per_instr_per_wave": round(c / (iters * 12), 2)}), flush=True)
+    # 5. MFMA rates (4 independent accumulators per wave, 4 waves per workgroup, 4 workgroups per CU)
+    fsink = torch.zeros(16, dtype=torch.float32, device=dev)
+    for shape, name, flop in ((0, "bf16_32x32x16", 2 * 32 * 32 * 16), (3, "bf16_16x16x32", 2 * 16 * 16 * 32),
+                              (1, "fp8_scaled_32x32x64", 2 * 32 * 32 * 64), (2, "fp8_scaled_16x16x128", 2 * 16 * 16 * 128)):
+        iters, grid = 2048, 1024
+        t = timed(lambda: check(lib.dsa_mb_mfma_rate(shape, iters, grid, ctypes.c_void_p(fsink.data_ptr()), st),
+                                "mfma_rate"))
+        total = flop * 4 * iters * grid * 4
+        peak = FP8_PEAK_TFLOPS if "fp8" in name else BF16_PEAK_TFLOPS
+        print(json.dumps({"micro": "mfma_rate", "shape": name, "TFLOPs": round(total / t / 1e12, 1),
+                          "frac_of_peak": round(total / t / 1e12 / peak, 3)}), flush=True)
+    # 6. summation precision of the scaled fp8 MFMA: products 2^p and +-1.875 in one output
+    out = torch.zeros(17 * 64, dtype=torch.float32, device=dev)
+    for sign in (1, -1):
+        check(lib.dsa_mb_fp8_mfma_sum(sign, ctypes.c_void_p(out.data_ptr()), st), "fp8_mfma_sum")
+        torch.cuda.synchronize()
+        got = out.view(17, 64)[:, 0].cpu().tolist()
+        exact = [2.0 ** p + sign * 1.875 for p in range(17)]
+        print(json.dumps({"micro": "fp8_mfma_sum", "small_product": sign * 1.875,
+                          "first_p_not_exact": next((p for p in range(17) if got[p] != exact[p]), None),
+                          "small_part_kept": {p: got[p] - 2.0 ** p for p in range(17)}}), flush=True)
 
 
 def cpu_model() -> str:
@@ -526,6 +623,9 @@ def main():
         sys.exit(2)
     if args.copy_calib:
         copy_calib()
+        return
+    if args.micro:
+        micro()
         return
     if args.config == 4:
         bench_prefill(args)

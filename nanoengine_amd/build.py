@@ -14,6 +14,9 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libdsa_amd.so"
+# measurement kernels for `bench.py --micro`, kept out of the product library
+MICROBENCH_SRC = "microbench.hip"
+MICROBENCH_LIB = PKG_DIR / "libdsa_microbench.so"
 SOURCES = ["capi.hip", "topk.hip", "indexer.hip", "sparse_mla.hip", "cache_store.hip",
            "indexer_prologue.hip", "prefill_logits.hip", "sparse_mla_prefill.hip",
            "prefill_topk.hip"]
@@ -73,6 +76,7 @@ def build(verbose: bool = False) -> Path:
         objs = [os.path.join(tmp, Path(s).stem + ".o") for s in SOURCES]
         cmds = [[hipcc(), *HIPCC_FLAGS, *PER_FILE_FLAGS[s], "-c", str(CSRC / s), "-o", o]
                 for s, o in zip(SOURCES, objs)]
+        cmds.append([hipcc(), *HIPCC_FLAGS, "-shared", str(CSRC / MICROBENCH_SRC), "-o", str(MICROBENCH_LIB)])
         with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
             list(pool.map(lambda c: _run(c, verbose), cmds))
         _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(LIB_PATH), *objs], verbose)

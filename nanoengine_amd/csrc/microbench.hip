@@ -1,0 +1,286 @@
+// Microbenchmarks behind the design decisions of the DSA kernels, for gfx950.
+// Not part of the product library: built as libdsa_microbench.so and run by
+// `python bench.py --micro`, which prints one JSON line per measurement.
+//
+//   page_read      random 8448-byte indexer pages read with coalesced 16-byte
+//                  loads (the filter pass's access pattern): the HBM read
+//                  ceiling of that pattern;
+//   row_gather     random 656-byte MLA rows copied into LDS with
+//                  global_load_lds_dwordx4, 41 loads per 64-row block, two
+//                  blocks in flight (the sparse MLA gather): its ceiling;
+//   lds_read       ds_read_b128 bandwidth of one CU at 4, 8 and 16 waves;
+//   valu_issue     cycles per independent VALU instruction of one wave at 1,
+//                  2 and 4 waves per SIMD (v_fma_f32, v_exp_f32);
+//   mfma_rate      dense matrix-core rate of the shapes the kernels use;
+//   fp8_mfma_sum   the summation precision of the scaled fp8 MFMA: one
+//                  product 2^p and one product +-1.875 in the same output: the
+//                  exact sum is 2^p +- 1.875; the instruction's result shows
+//                  how far below the largest product the sum keeps bits.
+//
+// Each entry returns 0 or a HIP error code; timing is done by the caller with
+// events around the launch, except where a kernel reports clock64 cycles.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int kPageBytes = 8448;
+constexpr int kRowBytes = 656;
+constexpr int kBlockBytes = 64 * kRowBytes;  // 41984 = 41 wave-wide 16-byte loads
+
+// Each wave reads pages page_ids[w * per_wave .. +per_wave) (per_wave <= 64)
+// in full, two pages in flight, the ids loaded up front.
+__global__ void __launch_bounds__(256) page_read_kernel(const uint8_t* __restrict__ pool,
+                                                        const int32_t* __restrict__ page_ids, int per_wave,
+                                                        int* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int my_id = lane < per_wave ? page_ids[w * per_wave + lane] : 0;
+  v4i acc = {0, 0, 0, 0};
+  auto load = [&](v4i (&x)[9], int i) {
+    const uint8_t* page = pool + (int64_t)__builtin_amdgcn_readlane(my_id, i) * kPageBytes;
+#pragma unroll
+    for (int u = 0; u < 9; ++u) {
+      const int off = (u * 64 + lane) * 16;
+      x[u] = off < kPageBytes ? *reinterpret_cast<const v4i*>(page + off) : v4i{0, 0, 0, 0};
+    }
+  };
+  v4i x0[9], x1[9];
+  if (per_wave > 0) load(x0, 0);
+  for (int i = 0; i < per_wave; i += 2) {
+    if (i + 1 < per_wave) load(x1, i + 1);
+#pragma unroll
+    for (int u = 0; u < 9; ++u) acc ^= x0[u];
+    if (i + 2 < per_wave) load(x0, i + 2);
+    if (i + 1 < per_wave) {
+#pragma unroll
+      for (int u = 0; u < 9; ++u) acc ^= x1[u];
+    }
+  }
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x7a5a5a5a) sink[0] = 1;
+}
+
+// A pseudo-random row in [0, nrows) of (block, lane): no memory access, so the
+// loop's only vector-memory operations are the copies.
+__device__ __forceinline__ int64_t random_row(uint64_t key, int64_t nrows) {
+  key += 0x9e3779b97f4a7c15ull;
+  key = (key ^ (key >> 30)) * 0xbf58476d1ce4e5b9ull;
+  key = (key ^ (key >> 27)) * 0x94d049bb133111ebull;
+  key ^= key >> 31;
+  return (int64_t)(key % (uint64_t)nrows);
+}
+
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+
+// One workgroup of 4 waves per CU gathers nblk blocks of 64 random rows into
+// two alternating LDS buffers (each wave 10 or 11 of the 41 loads per block),
+// waiting for a block only when the buffer comes round again.
+__global__ void __launch_bounds__(256) row_gather_kernel(const uint8_t* __restrict__ pool, int64_t nrows,
+                                                         int nblk, int* __restrict__ sink) {
+  extern __shared__ __align__(16) uint8_t sm[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int first = wave * 10 + (wave < 1 ? 0 : 1), cnt = wave < 1 ? 11 : 10;
+  v4i acc = {0, 0, 0, 0};
+  for (int n = 0; n < nblk; ++n) {
+    const int64_t r = random_row(((uint64_t)blockIdx.x * nblk + n) * 64 + lane, nrows);
+    const uint64_t rowp = reinterpret_cast<uint64_t>(pool + r * kRowBytes);
+    uint8_t* buf = sm + (n & 1) * kBlockBytes;
+    if (n >= 2) {
+      // block n-2 (this buffer's last use) has landed; block n-1 may still be in flight
+      if (cnt == 11) asm volatile("s_waitcnt vmcnt(11)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+      __syncthreads();
+      acc ^= *reinterpret_cast<const v4i*>(buf + 16 * tid);
+      __syncthreads();
+    }
+    for (int i = 0; i < cnt; ++i) {
+      const int c = 64 * (first + i) + lane;
+      const int rr = min(c / 41, 63);
+      const uint64_t g = __shfl(rowp, rr, 64) + 16 * (c - rr * 41);
+      dma16(reinterpret_cast<const void*>(g), (uint32_t)reinterpret_cast<uintptr_t>(buf + 1024 * (first + i)));
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  acc ^= *reinterpret_cast<const v4i*>(sm + 16 * tid);
+  if (acc[0] == 0x12345 && acc[1] == 7) sink[0] = acc[2];
+}
+
+// ds_read_b128 of 16 bytes per lane, 8 independent reads per iteration.
+__global__ void lds_read_kernel(int iters, int* __restrict__ sink, unsigned long long* __restrict__ cycles) {
+  __shared__ __align__(16) uint8_t buf[65536];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < 65536 / 4; i += blockDim.x) reinterpret_cast<int*>(buf)[i] = i;
+  __syncthreads();
+  const unsigned long long c0 = clock64();
+  v4i acc = {0, 0, 0, 0};
+  uint32_t a = (uint32_t)(tid * 16) & 65535u;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= *reinterpret_cast<const v4i*>(buf + ((a + u * 4096u) & 65535u));
+    a += 1024u * (blockDim.x / 64);
+    asm volatile("" : "+v"(a));
+  }
+  __syncthreads();
+  const unsigned long long c1 = clock64();
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x12345678) sink[0] = 1;
+  if (tid == 0) cycles[blockIdx.x] = c1 - c0;
+}
+
+// 12 independent chains of one VALU operation per lane; MODE 0 v_fma_f32, 1 v_exp_f32.
+template <int MODE>
+__global__ void valu_issue_kernel(int iters, float c, int* __restrict__ sink, unsigned long long* __restrict__ cycles) {
+  const int lane = threadIdx.x & 63;
+  float f[12];
+  float g = c * (float)lane;
+#pragma unroll
+  for (int i = 0; i < 12; ++i) f[i] = 0.001f * (float)(lane + i);
+  asm volatile("" : "+v"(g));
+  const unsigned long long c0 = clock64();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 12; ++i) f[i] = MODE == 0 ? fmaf(f[i], g, g) : __builtin_amdgcn_exp2f(f[i]);
+  }
+  const unsigned long long c1 = clock64();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 12; ++i) s += f[i];
+  if (s == 1.2345f) sink[0] = 1;
+  if ((threadIdx.x & 63) == 0) cycles[blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)] = c1 - c0;
+}
+
+// Four independent accumulators per wave. MODE 0: bf16 32x32x16; 1: scaled fp8
+// 32x32x64; 2: scaled fp8 16x16x128; 3: bf16 16x16x32.
+template <int MODE>
+__global__ void __launch_bounds__(256) mfma_rate_kernel(int iters, float* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  v16f a16[4];
+  v4f a4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a16[i][r] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a4[i][r] = 0.f;
+  }
+  const v4i x4 = {lane, lane + 1, lane + 2, lane + 3};
+  const v8i x8 = {lane, 1, 2, 3, 4, 5, 6, 7};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (MODE == 0)
+        a16[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x4), __builtin_bit_cast(v8bf, x4),
+                                                         a16[i], 0, 0, 0);
+      else if constexpr (MODE == 1)
+        a16[i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(x8, x8, a16[i], 0, 0, 0, 127, 0, 127);
+      else if constexpr (MODE == 2)
+        a4[i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x8, x8, a4[i], 0, 0, 0, 127, 0, 127);
+      else
+        a4[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, x4), __builtin_bit_cast(v8bf, x4),
+                                                        a4[i], 0, 0, 0);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += a16[i][r];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s += a4[i][r];
+  }
+  if (s == 1.2345f) sink[0] = s;
+}
+
+// Summation precision of the scaled fp8 MFMA. One wave, one 32x32x64 MFMA per
+// p = 0 .. 16: row 0 of A = q = (2^a, sign * 1.875, 0, ...), column 0 of B =
+// k = (2^(p-a), 1, 0, ...), a = min(p, 8), unit scales (on this instruction
+// the e8m0 scale of a row comes from one lane and covers all 64 k, so the two
+// products must be told apart by their fp8 values). The exact C[0][0] is
+// 2^p + sign * 1.875, exact in f32 for p <= 16; out[64 p] is the instruction's.
+__global__ void __launch_bounds__(64) fp8_mfma_sum_kernel(int sign, float* __restrict__ out) {
+  const int lane = threadIdx.x;
+  // A operand: lane l holds row l % 32, k-bytes 32 (l / 32) .. +31 (byte 0 of the first register first);
+  // B operand: lane l holds column l % 32, the same k-bytes. e4m3: 2^x = (x + 7) << 3, 1.875 = 0x3f,
+  // 1.0 = 0x38, sign bit 0x80.
+  for (int p = 0; p <= 16; ++p) {
+    const int a = p < 8 ? p : 8, b = p - a;
+    v8i A = {0, 0, 0, 0, 0, 0, 0, 0}, B = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (lane == 0) {
+      A[0] = ((a + 7) << 3) | ((sign < 0 ? 0xbf : 0x3f) << 8);
+      B[0] = ((b + 7) << 3) | (0x38 << 8);
+    }
+    v16f c = {};
+    c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, c, 0, 0, 0, 127, 0, 127);
+    // every lane stores (a store by lane 0 alone would let the compiler move the
+    // MFMA under a one-lane mask); C[0][0] is lane 0's register 0
+    out[p * 64 + lane] = c[0];
+  }
+}
+
+}  // namespace
+
+#define MB_API __attribute__((visibility("default")))
+
+extern "C" {
+
+MB_API int dsa_mb_page_read(const void* pool, const int32_t* page_ids, int per_wave, int grid, int* sink, void* stream) {
+  hipLaunchKernelGGL(page_read_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const uint8_t*>(pool), page_ids, per_wave, sink);
+  return (int)hipGetLastError();
+}
+
+MB_API int dsa_mb_row_gather(const void* pool, int64_t nrows, int nblk, int grid, int* sink, void* stream) {
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void*)row_gather_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             2 * kBlockBytes);
+    if (e != hipSuccess) return (int)e;
+    attr = true;
+  }
+  hipLaunchKernelGGL(row_gather_kernel, dim3(grid), dim3(256), 2 * kBlockBytes, (hipStream_t)stream,
+                     static_cast<const uint8_t*>(pool), nrows, nblk, sink);
+  return (int)hipGetLastError();
+}
+
+MB_API int dsa_mb_lds_read(int waves, int iters, int grid, int* sink, unsigned long long* cycles, void* stream) {
+  hipLaunchKernelGGL(lds_read_kernel, dim3(grid), dim3(64 * waves), 0, (hipStream_t)stream, iters, sink, cycles);
+  return (int)hipGetLastError();
+}
+
+MB_API int dsa_mb_valu_issue(int op, int threads, int iters, int grid, int* sink, unsigned long long* cycles, void* stream) {
+  if (op == 0)
+    hipLaunchKernelGGL(valu_issue_kernel<0>, dim3(grid), dim3(threads), 0, (hipStream_t)stream, iters, 1.f, sink,
+                       cycles);
+  else
+    hipLaunchKernelGGL(valu_issue_kernel<1>, dim3(grid), dim3(threads), 0, (hipStream_t)stream, iters, 1.f, sink,
+                       cycles);
+  return (int)hipGetLastError();
+}
+
+MB_API int dsa_mb_mfma_rate(int shape, int iters, int grid, float* sink, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  switch (shape) {
+    case 0: hipLaunchKernelGGL(mfma_rate_kernel<0>, dim3(grid), dim3(256), 0, st, iters, sink); break;
+    case 1: hipLaunchKernelGGL(mfma_rate_kernel<1>, dim3(grid), dim3(256), 0, st, iters, sink); break;
+    case 2: hipLaunchKernelGGL(mfma_rate_kernel<2>, dim3(grid), dim3(256), 0, st, iters, sink); break;
+    default: hipLaunchKernelGGL(mfma_rate_kernel<3>, dim3(grid), dim3(256), 0, st, iters, sink); break;
+  }
+  return (int)hipGetLastError();
+}
+
+MB_API int dsa_mb_fp8_mfma_sum(int sign, float* out, void* stream) {
+  hipLaunchKernelGGL(fp8_mfma_sum_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, sign, out);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"
