@@ -12,6 +12,7 @@ comparison is bit for bit, on:
     host-ordered fix-up: hot keys on the sampled positions (the list comes up
     short) and all-equal scores (the list overflows), with more deferred rows
     than one fix-up chunk holds;
+  * NaN keys and overflowing scores;
   * a small case against the oracle's logits and ragged top-k directly.
 """
 import numpy as np
@@ -165,3 +166,25 @@ def test_workspace_too_small_is_rejected(cuda):
     ws = torch.empty(need - 256, dtype=torch.uint8, device=cuda)
     with pytest.raises(RuntimeError, match="workspace"):
         ops.mqa_topk(q, kv, sc, w, ks, ke, 5000, out, workspace=ws)
+
+
+def test_nan_and_overflowing_scores_match_two_step(cuda):
+    """fp8 NaN codes in some keys (NaN logits rank lowest) and weights large
+    enough that some logits overflow to +-inf: the fused entry still returns
+    the two-step path's indices."""
+    print("mqa_topk NaN / inf scores", flush=True)
+    n = 20000
+    lens = [15000, 9000, 3000, 20000]
+    q, kv, sc, w = _inputs(cuda, len(lens), n, 10)
+    raw = kv.view(torch.uint8).clone()
+    g = torch.Generator(device=cuda).manual_seed(11)
+    nan_keys = torch.randint(0, n, (500,), device=cuda, generator=g)
+    raw[nan_keys, 5] = 0x7f                     # e4m3fn NaN
+    kv = raw.view(torch.float8_e4m3fn)
+    w = w.clone()
+    w[1] *= 1e36                                # row 1: many logits overflow to +-inf
+    ks, ke = _windows(cuda, lens, n, 12)
+    exp = _two_step(q, kv, sc, w, ks, ke, n)
+    got = _fused(q, kv, sc, w, ks, ke, n)
+    torch.cuda.synchronize()
+    assert torch.equal(got, exp)
