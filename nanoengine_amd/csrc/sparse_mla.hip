@@ -6,43 +6,40 @@
 // where kv(slot) is a 656-byte row [512 e4m3fn][4 x f32 tile scale][64 bf16].
 //
 // Workgroup = 8 waves (two per SIMD) = 64 heads of one token over one key
-// split. Two waves share each SIMD so that one wave's matrix work overlaps the
-// other's vector work: a single wave issues a vector instruction only every
-// ~7 cycles, so at one wave per SIMD this kernel would be bound by vector
-// issue, not by the matrix cores. Each wave fits in 256 registers.
-//
-// Wave w = (head half hp = w/4, quarter q = w%4); its 32 heads are
-// hp*32 + 0..31 of the workgroup's 64. Per block of 64 selected rows:
-//   gather : the raw 656-byte rows go straight from HBM into LDS with
+// split, in blocks of 64 selected rows. The waves specialise, so that each
+// SIMD pairs a wave in its score phase with a wave in its P.V phase instead
+// of two waves in the same phase:
+//   QK waves 0-3: wave (hp = w/2, kh = w%2) owns keys 32kh .. 32kh+31 of each
+//            block for the 32 heads of head half hp, over all 576 dims:
+//            S^T[32 keys x 32 heads] on 36 v_mfma_f32_32x32x16_bf16. A = the
+//            key's fp8 nope bytes from LDS converted to bf16 with the row's
+//            tile scale (v_cvt_scalef32_pk_bf16_fp8; exact, since an e4m3
+//            value times a power of two is a bf16 value) and its bf16 rope;
+//            B = the query's bf16 values as given, resident in registers.
+//            Products are exact and sums are f32, as in a bf16
+//            dequantise-then-multiply. (The scaled fp8 MFMA would take the
+//            raw rows directly, but it sums its 64 products to only ~13 bits
+//            below the largest one.) Then the wave's own online softmax over
+//            its 32 keys: a lazy reference m (an integer, log2 units) per
+//            head, P = 2^(s - m) to LDS as bf16, the reference beside it.
+//   PV waves 4-7: wave (hp, dh) owns O[32 heads of hp x dims 256dh .. +256]
+//            and adds the previous block's P.V: the two key halves' P come
+//            with their own references m0, m1; the wave keeps O against
+//            R = max(m0, m1) (rescaling O by a power of two when R moves) and
+//            forms P' = P * 2^(e + m_kh - R), e the tile scale exponent of
+//            each key, by adding to the bf16 exponent field; V is read from
+//            the raw rows with ds_read_b64_tr_b8 (8 keys x 1 dim per lane, the
+//            B operand layout) and converted with unit scale.
+//   rows   : the raw 656-byte rows go straight from HBM into LDS with
 //            global_load_lds_dwordx4 - consecutive lanes take consecutive
 //            16-byte pieces of the packed rows - into one of three buffers,
-//            two blocks ahead of use. The row indices arrive the same way,
+//            one block ahead of use (block t+1 while the QK waves read block t
+//            and the PV waves block t-1). The row indices arrive the same way,
 //            four blocks ahead, in a five-entry ring; one wave turns a block's
 //            indices into a 64-entry row-address table in LDS, so a load costs
 //            a table read and an add. Invalid indices read a zero row.
-//   QK     : wave (kh = q/2, d = q%2) forms the partial S^T[32 keys x 32
-//            heads] of keys 32kh..32kh+31 over nope dims [256d, 256d+256)
-//            and rope dims [32d, 32d+32), all on v_mfma_f32_32x32x16_bf16:
-//            A = the key's fp8 nope bytes from LDS converted to bf16 with the
-//            row's tile scale (v_cvt_scalef32_pk_bf16_fp8; exact, since an
-//            e4m3 value times a power of two is a bf16 value) and its bf16
-//            rope; B = the query's bf16 values as given. Products are exact
-//            and sums are f32, as in a bf16 dequantise-then-multiply. (The
-//            scaled fp8 MFMA would take the raw rows directly, but it sums its
-//            64 products to only ~14 bits below the largest one.)
-//   reduce : the two dim halves are summed by a reduce-scatter through LDS:
-//            wave (kh, d) ends with the full scores of keys 16o..16o+15,
-//            o = 2kh + d, so each score is exponentiated exactly once.
-//   softmax: per-head block maxima of the four key quarters are exchanged;
-//            online softmax in the exp2 domain with lazy rescaling (the
-//            running max moves only when a block raises it by more than 2^8).
-//            P goes to LDS once, as bf16.
-//   PV     : wave q produces output dims [128q, 128q+128) = V tile q of its
-//            32 heads: O += P' . V on v_mfma_f32_32x32x16_bf16, P' = P * 2^e
-//            with e the tile scale exponent of each key (a 16-bit add to the
-//            bf16 exponent field, read from a per-block table), V read from
-//            the raw rows with ds_read_b64_tr_b8 (8 keys x 1 dim per lane, the
-//            B operand layout) and converted with unit scale.
+// One barrier per block: P, the references and the next block's rows change
+// hands there; no score, maximum or sum is exchanged inside a block.
 // Splits over the key list (for small batches) write normalised partial
 // outputs and LSEs to a caller-provided workspace; a combine kernel merges
 // them with the LSE rule of merge_attention_states.
@@ -69,20 +66,24 @@ constexpr int kBufBytes = kMlaKeys * kMlaRowBytes;    // 41984: one block of pac
 constexpr int kDmaPerBlock = kBufBytes / 1024;        // 41 wave-wide 16-byte loads per block
 constexpr int kNumBufs = 3;
 // LDS map (bytes)
-constexpr int kXsOff = kNumBufs * kBufBytes;          // score partials: [8 waves][64 lanes][8 f32]
-constexpr int kMxOff = kXsOff + kMlaWaves * 64 * 32;  // block maxima / final sums: [2 hp][32 heads][4 quarters] f32
-constexpr int kPOff = kMxOff + 2 * 32 * 4 * 4;        // P: [2 hp][4 quarters][64 lanes][8 bf16]
-constexpr int kEOff = kPOff + 2 * 4 * 64 * 16;        // exponent offsets, two blocks: [2][4 tiles][4 k-steps][2 halves][8 u16]
-constexpr int kRingOff = kEOff + 2 * 4 * 4 * 2 * 16;  // row indices, one 64-entry block per slot
+constexpr int kPOff = kNumBufs * kBufBytes;            // P, two blocks: [2][2 hp][4 k-steps][64 lanes][8 bf16]
+constexpr int kEOff = kPOff + 2 * 2 * 4 * 64 * 16;     // exponent tables, one per PV wave: [4][2 tiles][4][2][8 u16]
+constexpr int kRefOff = kEOff + 4 * 512;               // references of the two key halves, two blocks: [2][2 hp][2][32] f32
+constexpr int kFinOff = kRefOff + 2 * 2 * 2 * 32 * 4;  // final sums, references, maxima: [3][2 hp][2][32] f32
+constexpr int kRingOff = kFinOff + 3 * 128 * 4;        // row indices, one 64-entry block per slot
 constexpr int kRingSlots = 5;
 constexpr int kAddrOff = kRingOff + kRingSlots * 256;  // row addresses of blocks being gathered, [2][64] u64
 constexpr size_t kMlaSmemBytes = kAddrOff + 2 * kMlaKeys * 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
-// Smallest P kept for a valid key (log2): P' = P * 2^e is formed by adding e to
-// the bf16 exponent field, which needs P to be a normal number.
-constexpr float kMinLogP = -60.0f;
+// P' = P * 2^(e + m_kh - R) is formed by adding to the bf16 exponent field,
+// which needs P' to stay a normal number: P of a valid key is kept at or above
+// 2^-30 of its key half's reference, and a key half more than 2^30 below the
+// other is left out of that block's P.V (its share is below 2^-22 of the
+// row's). With tile scales above 2^-66, P' stays above 2^-126.
+constexpr float kMinLogP = -30.0f;
+constexpr int kDropExp = -30;
 constexpr int kIdxWave = 7;                // the wave that fetches the row indices
 
 static_assert(kBufBytes % 1024 == 0, "a block of rows must be whole wave-wide loads");
@@ -113,7 +114,7 @@ struct MlaParams {
 
 // ---- asynchronous global -> LDS copies. They are issued from inline asm so
 // that the compiler neither inserts vmcnt(0) before every LDS read nor waits
-// for them at barriers: the kernel counts them itself with wait_vm().
+// for them at barriers: the kernel waits for them itself (vmcnt).
 // `lds` is the wave's destination base (M0); lane i writes lds + 4*size*i.
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
@@ -122,13 +123,6 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
-}
-// Wait until at most n of this wave's copies are outstanding (n in {0, 1, 5, 6}).
-__device__ __forceinline__ void wait_vm(int n) {
-  if (n >= 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-  else if (n == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
-  else if (n >= 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 __device__ __forceinline__ void barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -220,7 +214,7 @@ __device__ __forceinline__ int dma_first(int wave) {
   return wave * (kDmaPerBlock / kMlaWaves) + min(wave, kDmaPerBlock % kMlaWaves);
 }
 static_assert(kDmaPerBlock / kMlaWaves == 5 && kDmaPerBlock % kMlaWaves == 1,
-              "wait_vm() counts 6 / 5 loads per wave");
+              "six loads for wave 0, five for the others");
 
 // Load i of this lane: table byte offset 8 * row in bits 0-15, byte offset
 // within the row in bits 16-31.
@@ -274,335 +268,372 @@ __device__ __forceinline__ void issue_index(const MlaParams& P, uint8_t* smem, i
   dma4(src, __builtin_amdgcn_readfirstlane(lds_addr(smem + kRingOff + (j % kRingSlots) * 256)));
 }
 
+// Wave-uniform state of one workgroup's loop.
+struct MlaCtx {
+  int lane, wave, h, c32, hp, kh, t_tok, key_begin, nblk, h_half, head;
+  bool head_ok;
+};
+
+// Start of iteration t (both roles, every wave): with `compact`, the first
+// block without a valid index ends the loop there (nblk_eff = t: the P.V of
+// block t-1 still runs); the index load of block t+4; this wave's share of
+// block t+1's rows.
+__device__ __forceinline__ void iteration_start(const MlaParams& P, uint8_t* smem, const MlaCtx& c,
+                                                const DmaLanes& dl, int t, int& nblk_eff) {
+  if (P.compact && t < nblk_eff) {
+    const int32_t slot = reinterpret_cast<const int32_t*>(smem + kRingOff + (t % kRingSlots) * 256)[c.lane];
+    if (__ballot(slot_valid(P, slot)) == 0ull) nblk_eff = t;  // every wave reads the same indices
+  }
+  if (c.wave == kIdxWave && t + 4 < c.nblk) issue_index(P, smem, c.t_tok, c.key_begin, t + 4, c.lane);
+  if (t + 1 < nblk_eff) issue_block(smem, t + 1, dl, smem + ((t + 1) % kNumBufs) * kBufBytes, c.wave);
+}
+// End of iteration t: this wave's loads (block t+1's rows, index loads) have
+// landed; after the barrier every wave sees block t+1's rows and P(t).
+__device__ __forceinline__ void iteration_end() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  barrier();
+}
+
+// QK waves: S of block t over this wave's 32 keys, its lazy reference, P(t).
+__device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, const MlaCtx& c, const DmaLanes& dl) {
+  const int lane = c.lane, h = c.h, c32 = c.c32, hp = c.hp, kh = c.kh;
+  // the query as the B operand over all dims: nope chunk k (64 dims), k-step j =
+  // dims 64k + 32h + 8j .. +7, the same dims the key operand converts from its
+  // row bytes; rope k-step r = bf16 dims 512 + 16r + 8h .. +7
+  v4i qn[8][4];
+  v4i qr[4];
+  {
+    const uint16_t* qh = P.q + (int64_t)c.t_tok * P.q_tok_stride + (int64_t)(c.head_ok ? c.head : 0) * P.q_head_stride;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qn[k][j] = *reinterpret_cast<const v4i*>(qh + 64 * k + 32 * h + 8 * j);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) qr[r] = *reinterpret_cast<const v4i*>(qh + 512 + 16 * r + 8 * h);
+  }
+  // in registers before the loop: a wait the compiler places for these loads
+  // inside the loop would also wait for every copy in flight (0x0f70 = vmcnt(0))
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  float* ref = reinterpret_cast<float*>(smem + kRefOff);
+  float m_run = -__builtin_inff();  // this key half's reference per head c32 (an integer, log2 units)
+  float m_max = -__builtin_inff();  // exact running maximum (log2 units), for max_out
+  float l_run = 0.f;                // sum of P against m_run, this lane's keys only
+  int nblk_eff = c.nblk;
+
+  for (int t = 0; t <= nblk_eff; ++t) {
+    iteration_start(P, smem, c, dl, t, nblk_eff);
+    if (t < nblk_eff) {
+      const uint8_t* buf = smem + (t % kNumBufs) * kBufBytes;
+      const int32_t slot_t = reinterpret_cast<const int32_t*>(smem + kRingOff + (t % kRingSlots) * 256)[lane];
+      const uint64_t vmask = __ballot(slot_valid(P, slot_t));
+      // s[r]: key 32kh + 8(r/4) + 4h + r%4, head c32
+      v16f s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.f;
+      const uint8_t* row = buf + (32 * kh + c32) * kMlaRowBytes;
+      const v4f ksc = *reinterpret_cast<const v4f*>(row + 512);
+      const uint8_t* krow = row + 32 * h;
+      v8i kraw[2];
+      kraw[0] = lds_read32(krow);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (k + 1 < 8) kraw[(k + 1) & 1] = lds_read32(krow + 64 * (k + 1));
+        const float sc = ksc[k >> 1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v8i& kr = kraw[k & 1];
+          v4i kb;
+          kb[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j], sc, false));
+          kb[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j], sc, true));
+          kb[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j + 1], sc, false));
+          kb[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j + 1], sc, true));
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(kb), as_v8bf(qn[k][j]), s, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const v4i rope = *reinterpret_cast<const v4i*>(row + 528 + 32 * r + 16 * h);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(rope), as_v8bf(qr[r]), s, 0, 0, 0);
+      }
+      // invalid keys score -inf (their rows are zeros); the masks are skipped
+      // when every key of the block is valid, the usual case
+      const bool all_valid = vmask == ~0ull;
+      uint32_t vb16 = 0xffffu;  // bit r: key 32kh + 8(r/4) + 4h + r%4 valid
+      if (!all_valid) {
+        const uint64_t vm = vmask >> (32 * kh + 4 * h);
+        vb16 = (uint32_t)(vm & 0xfu) | ((uint32_t)((vm >> 8) & 0xfu) << 4) | ((uint32_t)((vm >> 16) & 0xfu) << 8) |
+               ((uint32_t)((vm >> 24) & 0xfu) << 12);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (!((vb16 >> r) & 1u)) s[r] = -__builtin_inff();
+      }
+      float mloc = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+      mloc = fmaxf(mloc, fmaxf(fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11])),
+                               fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]))));
+      mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+      const float mblk = mloc * P.scale_log2;
+      m_max = fmaxf(m_max, mblk);
+      // lazy reference: it moves (to an integer) only when a block exceeds it by 2^8
+      const bool need = mblk > m_run + kRescaleThreshold;
+      if (__ballot(need)) {
+        const float m_new = need ? ceilf(mblk) : m_run;
+        l_run *= __builtin_amdgcn_exp2f(m_run - m_new);  // a power of two (0 from -inf)
+        m_run = m_new;
+      }
+      const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
+      float pv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        pv[r] = __builtin_amdgcn_exp2f(fmaxf(fmaf(s[r], P.scale_log2, -m_use), kMinLogP));
+      if (!all_valid) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (!((vb16 >> r) & 1u)) pv[r] = 0.f;
+      }
+      float lsum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) lsum += pv[r];
+      l_run += lsum;
+      // P as the PV A operand of k-steps 2kh, 2kh+1: lane (c32, h) holds head
+      // c32, keys 16ks + 8(j/4) + 4h + j%4 (j = 0..7)
+      uint8_t* pb = smem + kPOff + (t & 1) * 8192 + hp * 4 * 1024;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const v4i pw = {cvt_pk_bf16(pv[8 * i], pv[8 * i + 1]), cvt_pk_bf16(pv[8 * i + 2], pv[8 * i + 3]),
+                        cvt_pk_bf16(pv[8 * i + 4], pv[8 * i + 5]), cvt_pk_bf16(pv[8 * i + 6], pv[8 * i + 7])};
+        *reinterpret_cast<v4i*>(pb + ((2 * kh + i) * 64 + lane) * 16) = pw;
+      }
+      if (h == 0) ref[(((t & 1) * 2 + hp) * 2 + kh) * 32 + c32] = m_run;
+    }
+    iteration_end();
+  }
+  // sums (both lane halves), references and maxima of this key half
+  float* fin = reinterpret_cast<float*>(smem + kFinOff);
+  const float l2 = l_run + shfl_xor(l_run, 32);
+  if (h == 0) {
+    fin[(hp * 2 + kh) * 32 + c32] = l2;
+    fin[128 + (hp * 2 + kh) * 32 + c32] = m_run;
+    fin[256 + (hp * 2 + kh) * 32 + c32] = m_max;
+  }
+  barrier();
+}
+
+// PV waves: O += P'(t-1) . V(t-1) against R, then the normalised output.
+__device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, const MlaCtx& c, const DmaLanes& dl,
+                                         int split) {
+  const int lane = c.lane, h = c.h, c32 = c.c32, hp = c.hp, dh = c.kh;
+  const float* ref = reinterpret_cast<const float*>(smem + kRefOff);
+  // this wave's exponent table (its two V tiles 2dh, 2dh+1): [2][4 k-steps][2 h][8 u16]
+  uint16_t* et = reinterpret_cast<uint16_t*>(smem + kEOff) + (c.wave - 4) * 256;
+  v16f o[8];  // o[nt][r]: head h_half + 8(r/4) + 4h + r%4, dim 256dh + 32nt + c32
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float R = -__builtin_inff();  // reference of O per head c32 (an integer, log2 units)
+  // transposing V reads: lane (G = lane/16, m = lane%16) addresses key row
+  // 8(e/4) + 4h + e%4 (e = m/2) and dims (G%2)*16 + 8(m%2) of each 32-dim tile
+  const int m16 = lane & 15, G = lane >> 4;
+  const int e8 = m16 >> 1;
+  const uint32_t vlane = (uint32_t)((8 * (e8 >> 2) + 4 * h + (e8 & 3)) * kMlaRowBytes + 256 * dh + (G & 1) * 16 +
+                                    8 * (m16 & 1));
+  int nblk_eff = c.nblk;
+
+  for (int t = 0; t <= nblk_eff; ++t) {
+    iteration_start(P, smem, c, dl, t, nblk_eff);
+    // row addresses of block t+2 (its indices landed two iterations ago); the
+    // table slot was last read when block t was issued, before this iteration
+    if (c.wave == kTabWave && t + 2 < c.nblk) build_addr_table(P, smem, t + 2, lane);
+    if (t >= 1) {
+      const int par = (t - 1) & 1;
+      const uint8_t* bufp = smem + ((t - 1) % kNumBufs) * kBufBytes;
+      {
+        // exponent table of block t-1, tiles 2dh and 2dh+1 (lane = key): the
+        // tile scale's exponent in the bf16 exponent field, at the PV A
+        // operand position of the key (k-step key/16, lane half (key/4)%2,
+        // element 4((key/8)%2) + key%4)
+        const int key = lane;
+        const uint2 sb = *reinterpret_cast<const uint2*>(bufp + key * kMlaRowBytes + 512 + 8 * dh);
+        const int pos = ((key >> 4) * 2 + ((key >> 2) & 1)) * 8 + 4 * ((key >> 3) & 1) + (key & 3);
+        et[pos] = (uint16_t)((uint32_t)((((int)((sb.x >> 23) & 0xffu)) - 127) << 7) & 0xffffu);
+        et[64 + pos] = (uint16_t)((uint32_t)((((int)((sb.y >> 23) & 0xffu)) - 127) << 7) & 0xffffu);
+      }
+      // O's reference follows the larger key-half reference; O moves by a power of two
+      const float m0 = ref[((par * 2 + hp) * 2 + 0) * 32 + c32];
+      const float m1 = ref[((par * 2 + hp) * 2 + 1) * 32 + c32];
+      const float mn = fmaxf(m0, m1);
+      const bool up = mn > R;
+      if (__ballot(up)) {
+        const float alpha = up ? __builtin_amdgcn_exp2f(R - mn) : 1.f;  // 0 from -inf
+        R = up ? mn : R;
+        int hb = 4 * h;
+        asm volatile("" : "+v"(hb));
+        float ar[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ar[r] = __shfl(alpha, 8 * (r >> 2) + hb + (r & 3), 64);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[nt][r] *= ar[r];
+      }
+      // per key half: m_kh - R (<= 0) for the bf16 exponent field, or left out
+      int fx[2];
+      bool drop[2];
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const float mk = k2 == 0 ? m0 : m1;
+        const bool none = mk == -__builtin_inff();  // no valid key in this half yet: its P are 0
+        const int f = none ? 0 : (int)(mk - R);
+        drop[k2] = none || f < kDropExp;
+        fx[k2] = (f << 7) & 0xffff;
+        fx[k2] |= fx[k2] << 16;
+      }
+      const uint8_t* pb = smem + kPOff + par * 8192 + hp * 4 * 1024;
+      const uint32_t vb = lds_addr(bufp) + vlane;
+      // The transposing reads take no immediate offset, so each address is
+      // formed from an opaque base right before use; otherwise all of them
+      // would be hoisted out of the loop into registers.
+      auto vaddr = [&](int it) {
+        uint32_t a = vb + (16 * (it >> 1)) * kMlaRowBytes + 128 * (it & 1);
+        asm volatile("" : "+v"(a));
+        return a;
+      };
+      // iteration it = (k-step ks = it/2, tile 2dh + it%2): its P, exponent
+      // and V reads issued one iteration ahead
+      v2i vq[2][4];
+      v4i pq[2], eq[2];
+      {
+        const uint32_t a0 = vaddr(0);
+#pragma unroll
+        for (int nn = 0; nn < 4; ++nn) vq[0][nn] = lds_read_tr8_at(a0 + 32 * nn);
+        pq[0] = *reinterpret_cast<const v4i*>(pb + lane * 16);
+        eq[0] = *reinterpret_cast<const v4i*>(et + h * 8);
+      }
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int ks = it >> 1, jj = it & 1;
+        const int cur = it & 1, nxt = cur ^ 1;
+        if (it + 1 < 8) {
+          const int ks1 = (it + 1) >> 1, jj1 = (it + 1) & 1;
+          const uint32_t a1 = vaddr(it + 1);
+#pragma unroll
+          for (int nn = 0; nn < 4; ++nn) vq[nxt][nn] = lds_read_tr8_at(a1 + 32 * nn);
+          pq[nxt] = *reinterpret_cast<const v4i*>(pb + (ks1 * 64 + lane) * 16);
+          eq[nxt] = *reinterpret_cast<const v4i*>(et + ((jj1 * 4 + ks1) * 2 + h) * 8);
+        }
+        const int k2 = ks >> 1;  // k-steps 0, 1: key half 0; 2, 3: key half 1
+        v4i pa;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // (bit_cast of a vector element reads element 0; copy to scalars first)
+          const int pe = pq[cur][e], ee = eq[cur][e];
+          const v2u16 sum = __builtin_bit_cast(v2u16, pe) + __builtin_bit_cast(v2u16, ee) +
+                            __builtin_bit_cast(v2u16, fx[k2]);
+          pa[e] = drop[k2] ? 0 : __builtin_bit_cast(int, sum);
+        }
+#pragma unroll
+        for (int nn = 0; nn < 4; ++nn)
+          o[4 * jj + nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa), fp8x8_to_bf16(vq[cur][nn]),
+                                                                   o[4 * jj + nn], 0, 0, 0);
+      }
+    }
+    iteration_end();
+  }
+  barrier();  // the QK waves' sums, references and maxima are in LDS
+  const float* fin = reinterpret_cast<const float*>(smem + kFinOff);
+  // total of P per head c32 against R, and the exact maximum
+  float lt = 0.f, mm = -__builtin_inff();
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2) {
+    const float lk = fin[(hp * 2 + k2) * 32 + c32];
+    const float mk = fin[128 + (hp * 2 + k2) * 32 + c32];
+    if (mk != -__builtin_inff()) lt += lk * __builtin_amdgcn_exp2f(mk - R);
+    mm = fmaxf(mm, fin[256 + (hp * 2 + k2) * 32 + c32]);
+  }
+  const bool any = lt > 0.f;
+  const float inv = any ? 1.f / lt : 0.f;
+  const float lse = any ? (R + __builtin_amdgcn_logf(lt)) * kLn2 : -__builtin_inff();
+  const int h_half = c.h_half;
+  if (h_half >= P.H) return;
+  int hb = 4 * h;
+  asm volatile("" : "+v"(hb));
+  if (P.splits == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
+      const float ir = __shfl(inv, 8 * (r >> 2) + hb + (r & 3), 64);
+      if (h_half + hr < P.H) {
+        uint16_t* orow = P.out + ((int64_t)c.t_tok * P.H + h_half + hr) * kMlaDv + 256 * dh + c32;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
+      }
+    }
+    if (dh == 0 && h == 0 && c.head_ok) {
+      if (P.lse) P.lse[(int64_t)c.t_tok * P.H + c.head] = lse;
+      if (P.max_out) P.max_out[(int64_t)c.t_tok * P.H + c.head] = any ? mm * kLn2 : -__builtin_inff();
+    }
+  } else {
+    const int64_t row0 = ((int64_t)split * P.T + c.t_tok) * P.H + h_half;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
+      const float ir = __shfl(inv, 8 * (r >> 2) + hb + (r & 3), 64);
+      if (h_half + hr < P.H) {
+        float* orow = P.ws_o + (row0 + hr) * kMlaDv + 256 * dh + c32;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) orow[32 * nt] = o[nt][r] * ir;
+      }
+    }
+    if (dh == 0 && h == 0 && c.head_ok) P.ws_lse[row0 + c32] = lse;
+  }
+}
+
 __global__ void __launch_bounds__(kMlaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 sparse_mla_kernel(const MlaParams P) {
   extern __shared__ __align__(16) uint8_t smem[];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = lane >> 5, c32 = lane & 31;
-  const int hp = wave >> 2, q4 = wave & 3;
-  const int kh = q4 >> 1, d = q4 & 1;  // QK: key half, dim half
-  const int o4 = 2 * kh + d;           // owned key quarter after the reduce-scatter
-  const int jt = q4;                   // PV: V tile (output dims [128 jt, 128 jt + 128))
-
+  MlaCtx c;
+  c.lane = threadIdx.x & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  c.h = c.lane >> 5;
+  c.c32 = c.lane & 31;
+  c.hp = (c.wave & 3) >> 1;
+  c.kh = c.wave & 1;
   // XCD-aware order: consecutive logical work items (the head groups and
   // splits of one token) land on the same XCD and share its L2.
   const int nwg = gridDim.x;
   int work = blockIdx.x;
   if ((nwg & 7) == 0) work = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
   const int per_tok = P.head_groups * P.splits;
-  const int t = work / per_tok;
+  c.t_tok = work / per_tok;
   const int rem = work % per_tok;
   const int hg = rem / P.splits;
   const int split = rem % P.splits;
   const int chunk = P.topk / P.splits;
-  const int key_begin = split * chunk;
-  const int nblk = chunk / kMlaKeys;
+  c.key_begin = split * chunk;
+  c.nblk = chunk / kMlaKeys;
+  c.h_half = hg * kMlaHeadsPerWG + c.hp * 32;
+  c.head = c.h_half + c.c32;
+  c.head_ok = c.head < P.H;
 
-  const int h_half = hg * kMlaHeadsPerWG + hp * 32;  // first head of this wave's 32
-  const int head = h_half + c32;                     // this lane's head (score columns)
-  const bool head_ok = head < P.H;
-
-  // The indices of blocks 0-3 are fetched first, so that their round trip
-  // overlaps the query's (the wait for the query below covers them too).
-  if (wave == kIdxWave)
-    for (int j = 0; j < 4 && j < nblk; ++j) issue_index(P, smem, t, key_begin, j, lane);
-
-  // Query B operands, bf16 as given: nope chunk c (64 dims), k-step j holds
-  // dims 256d + 64c + 32h + 8j .. +7 for lane half h, the same dims the key
-  // operand converts from its row bytes. Rope k-step rho: bf16 dims
-  // 32d + 16rho + 8h + 0..7.
-  v4i qn[4][4];
-  v4i qr[2];
-  {
-    const uint16_t* qh = P.q + (int64_t)t * P.q_tok_stride + (int64_t)(head_ok ? head : 0) * P.q_head_stride;
-    const v4i z = {0, 0, 0, 0};
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        qn[c][j] = head_ok ? *reinterpret_cast<const v4i*>(qh + 256 * d + 64 * c + 32 * h + 8 * j) : z;
-#pragma unroll
-    for (int rho = 0; rho < 2; ++rho)
-      qr[rho] = head_ok ? *reinterpret_cast<const v4i*>(qh + 512 + 32 * d + 16 * rho + 8 * h) : z;
-  }
-  // The query must be in registers before the first copy is issued: a wait
-  // the compiler places for these loads inside the block loop would also wait
-  // for every copy in flight. (The builtin, unlike inline asm, is seen by the
-  // compiler's wait bookkeeping.) 0x0f70 = vmcnt(0) only.
-  __builtin_amdgcn_s_waitcnt(0x0f70);
-
-  v16f o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
-  float m_run = -__builtin_inff();  // per head c32, log2 domain (identical in the 4 waves of a head half)
-  float m_max = -__builtin_inff();  // exact running maximum (log2 domain), for max_out
-  float l_run = 0.f;                // per head c32: this lane's 8 keys of each block only
-
-  const int my_dma = dma_count(wave);
-  // prologue: the indices of blocks 0-3 have landed (issued first, waited
-  // for with the query); then the rows of blocks 0 and 1
-  barrier();
-  const DmaLanes dl = dma_lanes(wave, lane);
-  if (wave == kTabWave) {
-    build_addr_table(P, smem, 0, lane);
-    if (nblk > 1) build_addr_table(P, smem, 1, lane);
+  // prologue: the indices of blocks 0-3, the address tables of blocks 0 and
+  // 1, block 0's rows
+  if (c.wave == kIdxWave) {
+    for (int j = 0; j < 4 && j < c.nblk; ++j) issue_index(P, smem, c.t_tok, c.key_begin, j, c.lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   barrier();
-  issue_block(smem, 0, dl, smem, wave);
-  if (nblk > 1) issue_block(smem, 1, dl, smem + kBufBytes, wave);
-  // rows of block 0 have landed
-  wait_vm(nblk > 1 ? my_dma : 0);
-  barrier();
-
-  float* xs_mine = reinterpret_cast<float*>(smem + kXsOff) + (wave * 64 + lane) * 8;
-  const float* xs_part = reinterpret_cast<const float*>(smem + kXsOff) + ((wave ^ 1) * 64 + lane) * 8;
-  float* mx = reinterpret_cast<float*>(smem + kMxOff) + (hp * 32 + c32) * 4;
-  uint8_t* pbuf = smem + kPOff + hp * 4 * 1024;
-  uint16_t* etab = reinterpret_cast<uint16_t*>(smem + kEOff);
-
-  for (int n = 0; n < nblk; ++n) {
-    // Block n's rows landed (and are visible) at the last barrier of block n-1.
-    // The buffers, tables and rings a wave touches before its first barrier of
-    // block n are ones no wave still in block n-1 reads: the exponent and address
-    // tables are double-buffered by block parity.
-    const uint8_t* buf = smem + (n % kNumBufs) * kBufBytes;
-    const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kRingOff + (n % kRingSlots) * 256)[lane];
-    const uint64_t vmask = __ballot(slot_valid(P, slot_n));
-    // every wave reads the same indices, so all of them leave at the same block
-    if (P.compact && vmask == 0ull) break;
-    if (wave == kIdxWave && n + 4 < nblk) issue_index(P, smem, t, key_begin, n + 4, lane);
-    // row addresses of block n+2 (its indices landed before the last barrier), read after B3
-    if (wave == kTabWave && n + 2 < nblk) build_addr_table(P, smem, n + 2, lane);
-    uint16_t* et = etab + (n & 1) * 256;
-
-    // Exponent table of this block: entry (tile, key) = the tile scale's
-    // exponent shifted into the bf16 exponent field, at the position the PV
-    // A operand holds that key (k-step key/16, lane half (key/4)%2, element
-    // 4((key/8)%2) + key%4).
-    if (wave < 4) {
-      const int key = lane, tile = wave;
-      const uint32_t sb = *reinterpret_cast<const uint32_t*>(buf + key * kMlaRowBytes + 512 + 4 * tile);
-      const int e = (int)((sb >> 23) & 0xffu) - 127;
-      const int pos = ((tile * 4 + (key >> 4)) * 2 + ((key >> 2) & 1)) * 8 + 4 * ((key >> 3) & 1) + (key & 3);
-      et[pos] = (uint16_t)((uint32_t)(e << 7) & 0xffffu);
-    }
-
-    // ---- partial S^T[32 keys x 32 heads] over this wave's dims:
-    // s[r] = key 32kh + 8(r/4) + 4h + r%4, head c32
-    v16f s;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.f;
-    {
-      const uint8_t* row = buf + (32 * kh + c32) * kMlaRowBytes;
-      const v2f ksc = *reinterpret_cast<const v2f*>(row + 512 + 8 * d);
-      // K chunk c: lane half h holds bytes 256d + 64c + 32h .. +32 of key
-      // 32kh + c32, dequantised to bf16 with the tile scale (exact: an e4m3
-      // value times a power of two is a bf16 value), 8 per k-step
-      const uint8_t* krow = row + 256 * d + 32 * h;
-      v8i kraw[2];
-      kraw[0] = lds_read32(krow);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (c + 1 < 4) kraw[(c + 1) & 1] = lds_read32(krow + 64 * (c + 1));
-        const float sc = ksc[c >> 1];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const v8i& kr = kraw[c & 1];
-          v4i kb;
-          kb[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j], sc, false));
-          kb[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j], sc, true));
-          kb[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j + 1], sc, false));
-          kb[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kr[2 * j + 1], sc, true));
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(kb), as_v8bf(qn[c][j]), s, 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int rho = 0; rho < 2; ++rho) {
-        const v4i rope = *reinterpret_cast<const v4i*>(row + 528 + 64 * d + 32 * rho + 16 * h);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(rope), as_v8bf(qr[rho]), s, 0, 0, 0);
-      }
-    }
-
-    // ---- reduce-scatter with the dim partner (wave ^ 1): this wave keeps
-    // s[8d .. 8d+7] = keys 16 o4 + 8(i/4) + 4h + i%4 (i = 0..7) and sends the rest.
-    float sv[8];
-    if (d == 0) {
-      *reinterpret_cast<v4f*>(xs_mine) = v4f{s[8], s[9], s[10], s[11]};
-      *reinterpret_cast<v4f*>(xs_mine + 4) = v4f{s[12], s[13], s[14], s[15]};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) sv[i] = s[i];
-    } else {
-      *reinterpret_cast<v4f*>(xs_mine) = v4f{s[0], s[1], s[2], s[3]};
-      *reinterpret_cast<v4f*>(xs_mine + 4) = v4f{s[4], s[5], s[6], s[7]};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) sv[i] = s[8 + i];
-    }
-    barrier();  // B1
-    {
-      const v4f a = *reinterpret_cast<const v4f*>(xs_part);
-      const v4f b = *reinterpret_cast<const v4f*>(xs_part + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sv[i] += a[i];
-        sv[4 + i] += b[i];
-      }
-    }
-    // invalid keys score -inf (their rows are zeros, so P' . V gets exact zeros)
-    const uint64_t vm = vmask >> (16 * o4 + 4 * h);
-    if (vmask != ~0ull) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (!((vm >> (8 * (i >> 2) + (i & 3))) & 1ull)) sv[i] = -__builtin_inff();
-    }
-    float mloc = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-    mloc = fmaxf(mloc, shfl_xor(mloc, 32));
-    if (h == 0) mx[o4] = mloc;
-    barrier();  // B2
-
-    // ---- online softmax (exp2 domain), lazy rescale; the block maximum is
-    // the same in the four waves of a head half, so are m_run and alpha
-    {
-      const v4f m4 = *reinterpret_cast<const v4f*>(mx);
-      const float mblk = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])) * P.scale_log2;
-      m_max = fmaxf(m_max, mblk);
-      const bool need = mblk > m_run + kRescaleThreshold;  // true on the first valid block
-      if (__ballot(need)) {
-        const float m_new = need ? mblk : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
-        l_run *= alpha;
-        m_run = m_new;
-        // o rows are heads 8(r/4) + 4h + r%4
-        int hh = 4 * h;
-        asm volatile("" : "+v"(hh));
-        float ar[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ar[r] = __shfl(alpha, 8 * (r >> 2) + hh + (r & 3), 64);
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[nt][r] *= ar[r];
-      }
-    }
-    // m_run is -inf only while every key so far was invalid; then p = 0
-    const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
-    float pv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      pv[i] = __builtin_amdgcn_exp2f(fmaxf(fmaf(sv[i], P.scale_log2, -m_use), kMinLogP));
-    if (vmask != ~0ull) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (!((vm >> (8 * (i >> 2) + (i & 3))) & 1ull)) pv[i] = 0.f;
-    }
-    l_run += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-    {
-      const v4i pw = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]), cvt_pk_bf16(pv[4], pv[5]),
-                      cvt_pk_bf16(pv[6], pv[7])};
-      *reinterpret_cast<v4i*>(pbuf + (o4 * 64 + lane) * 16) = pw;
-    }
-    // rows of block n+1 have landed: issued at the end of block n-1 (or in the
-    // prologue); only the index wave's load of block n+4 went out after them
-    if (n + 1 < nblk) wait_vm(wave == kIdxWave && n + 4 < nblk ? 1 : 0);
-    barrier();  // B3
-
-    // ---- O[32 heads x 128 dims] += P' . V over the block's 64 keys (four k-steps of 16).
-    // Lane (group G = lane/16, m = lane%16) addresses key row 8(e/4) + 4h + e%4
-    // (e = m/2) and dims (G%2)*16 + 8(m%2) of each 32-dim tile.
-    {
-      const int m16 = lane & 15, G = lane >> 4;
-      const int e8 = m16 >> 1;
-      const uint8_t* vb = buf + (8 * (e8 >> 2) + 4 * h + (e8 & 3)) * kMlaRowBytes + 128 * jt + (G & 1) * 16 +
-                          8 * (m16 & 1);
-      // The transposing reads take no immediate offset, so each address is
-      // formed from an opaque base right before use; otherwise all of them
-      // would be hoisted out of the block loop into registers.
-      auto vstep = [&](int ks) {
-        uint32_t a = lds_addr(vb) + (16 * ks) * kMlaRowBytes;
-        asm volatile("" : "+v"(a));
-        return a;
-      };
-      v2i vr[2][4];
-      {
-        const uint32_t p = vstep(0);
-#pragma unroll
-        for (int nn = 0; nn < 4; ++nn) vr[0][nn] = lds_read_tr8_at(p + 32 * nn);
-      }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (ks + 1 < 4) {
-          const uint32_t p = vstep(ks + 1);
-#pragma unroll
-          for (int nn = 0; nn < 4; ++nn) vr[(ks + 1) & 1][nn] = lds_read_tr8_at(p + 32 * nn);
-        }
-        const v4i pr = *reinterpret_cast<const v4i*>(pbuf + (ks * 64 + lane) * 16);
-        const v4i ev = *reinterpret_cast<const v4i*>(et + ((jt * 4 + ks) * 2 + h) * 8);
-        v4i pa;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // (bit_cast of a vector element reads element 0; copy to scalars first)
-          const int pe = pr[e], ee = ev[e];
-          pa[e] = __builtin_bit_cast(int, __builtin_bit_cast(v2u16, pe) + __builtin_bit_cast(v2u16, ee));
-        }
-        v8bf vb16[4];
-#pragma unroll
-        for (int nn = 0; nn < 4; ++nn) vb16[nn] = fp8x8_to_bf16(vr[ks & 1][nn]);
-#pragma unroll
-        for (int nn = 0; nn < 4; ++nn)
-          o[nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa), vb16[nn], o[nn], 0, 0, 0);
-      }
-    }
-    // block n+2's rows, into the buffer of block n-1, which every wave left before B3
-    if (n + 2 < nblk) issue_block(smem, n + 2, dl, smem + ((n + 2) % kNumBufs) * kBufBytes, wave);
+  const DmaLanes dl = dma_lanes(c.wave, c.lane);
+  if (c.wave == kTabWave) {
+    build_addr_table(P, smem, 0, c.lane);
+    if (c.nblk > 1) build_addr_table(P, smem, 1, c.lane);
   }
-
-  // drain: nothing may be left in flight when the workgroup ends
+  barrier();
+  issue_block(smem, 0, dl, smem, c.wave);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // total of P per head: both lane halves, then the four key quarters
-  l_run += shfl_xor(l_run, 32);
-  barrier();
-  if (h == 0) mx[o4] = l_run;
-  barrier();
-  {
-    const v4f l4 = *reinterpret_cast<const v4f*>(mx);
-    l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
-  }
-  if (h_half >= P.H) return;
-  const bool any = l_run > 0.f;
-  const float inv = any ? 1.f / l_run : 0.f;
-  const float lse = any ? (m_run + __builtin_amdgcn_logf(l_run)) * kLn2 : -__builtin_inff();
-  // o[nt][r]: head h_half + 8(r/4) + 4h + r%4, dim 128 jt + 32nt + c32
-  if (P.splits == 1) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
-      const float ir = __shfl(inv, hr, 64);
-      if (h_half + hr < P.H) {
-        uint16_t* orow = P.out + ((int64_t)t * P.H + h_half + hr) * kMlaDv + 128 * jt + c32;
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
-      }
-    }
-    if (h == 0 && jt == 0 && head_ok && P.lse) P.lse[(int64_t)t * P.H + head] = lse;
-    if (h == 0 && jt == 0 && head_ok && P.max_out)
-      P.max_out[(int64_t)t * P.H + head] = any ? m_max * kLn2 : -__builtin_inff();
-  } else {
-    const int64_t row0 = ((int64_t)split * P.T + t) * P.H + h_half;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
-      const float ir = __shfl(inv, hr, 64);
-      if (h_half + hr < P.H) {
-        float* orow = P.ws_o + (row0 + hr) * kMlaDv + 128 * jt + c32;
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) orow[32 * nt] = o[nt][r] * ir;
-      }
-    }
-    if (h == 0 && jt == 0 && head_ok) P.ws_lse[row0 + c32] = lse;
-  }
+  barrier();  // block 0's rows are in LDS
+  // both roles run the same number of iterations and barriers
+  if (c.wave < 4) qk_waves(P, smem, c, dl);
+  else pv_waves(P, smem, c, dl, split);
 }
 
 // One 64-thread workgroup per (token, head): merge the split partials.
