@@ -43,6 +43,7 @@
 // Splits over the key list (for small batches) write normalised partial
 // outputs and LSEs to a caller-provided workspace; a combine kernel merges
 // them with the LSE rule of merge_attention_states.
+#include <algorithm>
 #include <cmath>
 
 #include "dsa_common.h"
@@ -677,10 +678,15 @@ int dsa_sparse_mla_num_splits(int num_tokens, int num_heads, int topk, int num_c
   if (num_cus <= 0) num_cus = 256;
   const int groups = (num_heads + dsa::kMlaHeadsPerWG - 1) / dsa::kMlaHeadsPerWG;
   const int64_t base = (int64_t)num_tokens * groups;
+  // A workgroup's time is a fixed start-up plus a cost per 64-row block, and
+  // one workgroup runs per CU at a time: split as far as the grid still fits
+  // the CUs in one round (a second round costs a whole workgroup's time), and
+  // keep at least 4 blocks per workgroup (below that the start-up and the
+  // combine outweigh the shorter key list). Splits must divide topk into
+  // 64-row blocks.
+  const int max_splits = std::min(8, topk / dsa::kMlaKeys);
   int splits = 1;
-  const int max_splits = topk / dsa::kMlaKeys;
-  // grow until the grid covers the CUs once; splits must divide topk into 64-row blocks
-  while (base * splits < num_cus && splits * 2 <= max_splits && (topk / (splits * 2)) % dsa::kMlaKeys == 0)
+  while (splits * 2 <= max_splits && base * splits * 2 <= num_cus && (topk / (splits * 2)) % dsa::kMlaKeys == 0)
     splits *= 2;
   return splits;
 }

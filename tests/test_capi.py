@@ -86,6 +86,8 @@ def test_workspace_size_queries(lib):
     # splits grow until the grid (64 heads per workgroup) covers the CUs, in 64-row blocks of top-k
     assert lib.dsa_sparse_mla_num_splits(128, 128, 2048, 256) == 1
     assert lib.dsa_sparse_mla_num_splits(32, 128, 2048, 256) == 4
+    assert lib.dsa_sparse_mla_num_splits(96, 128, 2048, 256) == 1   # two rounds of workgroups cost more
+    assert lib.dsa_sparse_mla_num_splits(4, 128, 2048, 256) == 8    # at least 4 blocks per workgroup
     assert lib.dsa_sparse_mla_num_splits(1, 16, 128, 256) == 2
 
 
