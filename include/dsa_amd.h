@@ -379,8 +379,9 @@ DSA_API int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, i
  *   fresh      [total_q, 576] bf16 (row stride fresh_row_stride elements)
  *   workspace  dsa_sparse_mla_prefill_paged_workspace_bytes(num_tokens, topk)
  * Same result as assembling the keys (dsa_mla_prefill_kv) and calling
- * dsa_sparse_mla_prefill, up to the summation order (and one bf16 rounding of
- * the cached part before the merge).
+ * dsa_sparse_mla_prefill, up to the summation order: one kernel runs each
+ * token's cached keys (fp8 rows, dequantised exactly in registers) and then its
+ * fresh bf16 rows under one softmax.
  * Replaces, at dlengine/runtime/models/deepseek_v2/deepseek_v2.py:1573-1650, the
  * key assembly (_gather_cache_cached_only, restore_mla_fp8_cache_rows,
  * _interleave_cached_fresh: layers/backends/attention/mla_utils.py:118-236)

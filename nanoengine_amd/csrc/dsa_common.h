@@ -144,11 +144,24 @@ int launch_mqa_logits(bool filter, const uint8_t* q, const uint8_t* kv, const fl
 // dsa_sparse_mla_decode). max_out (splits == 1 only) receives each head's
 // largest scaled score in natural units; with compact set, each row's valid
 // indices must come first and a workgroup stops at its first block with none.
+// A chunked prefill's keys for the sparse MLA decode kernel: token t attends
+// over the first counts[2t] entries of its cache-slot list (valid slots first)
+// and over counts[2t+1] fresh bf16 rows rows[idx[t][i]] (row stride in
+// elements, num_rows rows; idx row stride idx_stride, width >= counts rounded
+// up to 32).
+struct MlaFresh {
+  const int32_t* counts;
+  const void* rows;
+  int64_t row_stride;
+  int64_t num_rows;
+  const int32_t* idx;
+  int64_t idx_stride;
+};
 int sparse_mla_decode_impl(const void* q, int64_t q_token_stride, int64_t q_head_stride, const uint8_t* kv_cache,
                            int64_t kv_block_stride_bytes, int kv_block_size, int64_t kv_num_blocks,
                            const int32_t* indices, int64_t idx_stride, int num_tokens, int num_heads, int topk,
                            float sm_scale, void* out, float* lse, int num_splits, void* workspace,
-                           size_t workspace_bytes, void* stream, float* max_out, int compact);
+                           size_t workspace_bytes, void* stream, float* max_out, const MlaFresh* fresh);
 
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {

@@ -40,6 +40,11 @@
 //            a table read and an add. Invalid indices read a zero row.
 // One barrier per block: P, the references and the next block's rows change
 // hands there; no score, maximum or sum is exchanged inside a block.
+// Chunked prefill: after a token's cache-slot blocks come blocks of 32 fresh
+// bf16 rows [576] (the chunk's own keys, not yet in the cache). They go to LDS
+// the same way; the key half 0 QK waves read them as bf16 operands, and the
+// PV waves read V with ds_read_b64_tr_b16 (no tile scale), so cached and
+// fresh keys share one softmax.
 // Splits over the key list (for small batches) write normalised partial
 // outputs and LSEs to a caller-provided workspace; a combine kernel merges
 // them with the LSE rule of merge_attention_states.
@@ -64,6 +69,13 @@ constexpr int kMlaRowBytes = 656;
 constexpr int kMlaRowPieces = kMlaRowBytes / 16;      // 41
 constexpr int kMlaDv = 512;
 constexpr int kBufBytes = kMlaKeys * kMlaRowBytes;    // 41984: one block of packed raw rows
+// A chunked prefill's fresh keys are bf16 rows [576] (1152 B), 32 to a block:
+// a fresh block is 36 wave-wide loads and fits a row buffer.
+constexpr int kFreshKeys = 32;
+constexpr int kFreshRowBytes = 576 * 2;
+constexpr int kFreshRowPieces = kFreshRowBytes / 16;  // 72
+constexpr int kFreshDma = kFreshKeys * kFreshRowBytes / 1024;  // 36
+static_assert(kFreshKeys * kFreshRowBytes <= kBufBytes, "a fresh block must fit a row buffer");
 constexpr int kDmaPerBlock = kBufBytes / 1024;        // 41 wave-wide 16-byte loads per block
 constexpr int kNumBufs = 3;
 // LDS map (bytes)
@@ -90,8 +102,8 @@ constexpr int kIdxWave = 7;                // the wave that fetches the row indi
 static_assert(kBufBytes % 1024 == 0, "a block of rows must be whole wave-wide loads");
 static_assert(kMlaSmemBytes <= 160 * 1024, "LDS budget");
 
-// Source of the pieces of an invalid row: 656 zero bytes.
-__device__ __align__(16) uint8_t g_mla_zero_row[kMlaRowBytes];
+// Source of the pieces of an invalid row (cache or fresh): zero bytes.
+__device__ __align__(16) uint8_t g_mla_zero_row[kFreshRowBytes];
 
 struct MlaParams {
   const uint16_t* q;
@@ -110,7 +122,16 @@ struct MlaParams {
   float* ws_o;    // [splits, T, H, 512] (splits > 1)
   float* ws_lse;  // [splits, T, H]
   float* max_out; // [T, H] largest scaled score (natural units), or null (splits == 1 only)
-  int compact;    // the valid indices of a row come first: stop at the first block with none
+  // chunked prefill (paged, splits == 1): token t attends over ceil(counts[2t] / 64)
+  // blocks of cache slots from idx (valid slots first), then ceil(counts[2t+1] / 32)
+  // blocks of fresh bf16 rows fresh[fresh_idx[t][i]] (null counts: topk / splits
+  // blocks of cache slots)
+  const int32_t* counts;
+  const uint16_t* fresh;
+  int64_t fresh_row_stride;  // elements
+  int64_t fresh_rows;
+  const int32_t* fresh_idx;
+  int64_t fresh_idx_stride;
 };
 
 // ---- asynchronous global -> LDS copies. They are issued from inline asm so
@@ -145,6 +166,17 @@ __device__ __forceinline__ v2i lds_read_tr8(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)p);
 }
 
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+// Four 16-bit elements per lane, transposed within each 16-lane group: lane m
+// addresses row m/4, elements 4(m%4) .. +3 of a 4 x 16 tile and receives
+// column m of its four rows.
+__device__ __forceinline__ v4s lds_read_tr16_at(uint32_t a) {
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)a);
+}
+
 __device__ __forceinline__ v2i lds_read_tr8_at(uint32_t a) {
   typedef __attribute__((address_space(3))) v2i lds_v2i;
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(uintptr_t)a);
@@ -176,6 +208,13 @@ __device__ __forceinline__ v8i lds_read32(const uint8_t* p) {
 // pairs are loop invariants, computed once per lane (DmaLanes).
 constexpr int kTabWave = 6;  // the wave that builds the row-address table
 
+// Wave-uniform state of one workgroup's loop. Blocks [0, ncached) are 64 cache
+// slots each, blocks [ncached, nblk) 32 fresh bf16 rows each.
+struct MlaCtx {
+  int lane, wave, h, c32, hp, kh, t_tok, key_begin, nblk, ncached, h_half, head;
+  bool head_ok;
+};
+
 // Cache block of a physical slot.
 __device__ __forceinline__ int64_t slot_block(const MlaParams& P, int32_t slot) {
   return P.kv_block_shift >= 0 ? (int64_t)(slot >> P.kv_block_shift) : (int64_t)(slot / P.kv_block_size);
@@ -200,10 +239,24 @@ __device__ __forceinline__ uint64_t row_address(const MlaParams& P, int32_t slot
   return reinterpret_cast<uint64_t>(P.kv + blk * P.kv_blk_stride + in_blk * kMlaRowBytes);
 }
 
+// A fresh row index is used when it is in [0, fresh_rows); a fresh block's
+// ring entries 32-63 are never used.
+__device__ __forceinline__ bool fresh_valid(const MlaParams& P, int32_t r, int lane) {
+  return lane < kFreshKeys && r >= 0 && r < P.fresh_rows;
+}
+
 // Table of block j's row addresses from ring slot j % 5 (lane = row), in table j % 2.
-__device__ __forceinline__ void build_addr_table(const MlaParams& P, uint8_t* smem, int j, int lane) {
+template <bool kFresh>
+__device__ __forceinline__ void build_addr_table(const MlaParams& P, uint8_t* smem, const MlaCtx& c, int j) {
+  const int lane = c.lane;
   const int32_t slot = reinterpret_cast<const int32_t*>(smem + kRingOff + (j % kRingSlots) * 256)[lane];
-  *reinterpret_cast<uint64_t*>(smem + kAddrOff + (j & 1) * 512 + 8 * lane) = row_address(P, slot);
+  uint64_t a;
+  if (!kFresh || j < c.ncached)
+    a = row_address(P, slot);
+  else
+    a = fresh_valid(P, slot, lane) ? reinterpret_cast<uint64_t>(P.fresh + (int64_t)slot * P.fresh_row_stride)
+                                   : reinterpret_cast<uint64_t>(g_mla_zero_row);
+  *reinterpret_cast<uint64_t*>(smem + kAddrOff + (j & 1) * 512 + 8 * lane) = a;
 }
 
 // Wave w sends loads [first(w), first(w) + count(w)) of the block: six for
@@ -263,30 +316,45 @@ __device__ __forceinline__ void issue_block(const uint8_t* smem, int j, const Dm
   }
 }
 
-__device__ __forceinline__ void issue_index(const MlaParams& P, uint8_t* smem, int t, int key_begin, int j,
-                                            int lane) {
-  const int32_t* src = P.idx + (int64_t)t * P.idx_stride + key_begin + j * kMlaKeys + lane;
+// A fresh block's 36 loads: five each for waves 0-3, four for waves 4-7; lane l
+// of load i takes piece c = 64(first + i) + l of the packed 32 rows.
+__device__ __forceinline__ void issue_fresh_block(const uint8_t* smem, int j, const uint8_t* buf, int wave,
+                                                  int lane) {
+  const uint8_t* tab = smem + kAddrOff + (j & 1) * 512;
+  const int first = wave < 4 ? 5 * wave : 20 + 4 * (wave - 4);
+  const int cnt = wave < 4 ? 5 : 4;
+  for (int i = 0; i < cnt; ++i) {
+    const int pc = 64 * (first + i) + lane;
+    const int r = pc / kFreshRowPieces;
+    const uint64_t g = *reinterpret_cast<const uint64_t*>(tab + 8 * r) + 16 * (pc - r * kFreshRowPieces);
+    dma16(reinterpret_cast<const void*>(g), lds_addr(buf + 1024 * (first + i)));
+  }
+}
+static_assert(4 * 5 + 4 * 4 == kFreshDma, "fresh block loads per wave");
+
+// The row indices of block j into ring slot j % 5: 64 cache slots, or 32 fresh
+// row indices (lanes 32-63 repeat lanes 0-31).
+template <bool kFresh>
+__device__ __forceinline__ void issue_index(const MlaParams& P, uint8_t* smem, const MlaCtx& c, int j) {
+  const int32_t* src =
+      !kFresh || j < c.ncached ? P.idx + (int64_t)c.t_tok * P.idx_stride + c.key_begin + j * kMlaKeys + c.lane
+                    : P.fresh_idx + (int64_t)c.t_tok * P.fresh_idx_stride + (j - c.ncached) * kFreshKeys +
+                          (c.lane & (kFreshKeys - 1));
   dma4(src, __builtin_amdgcn_readfirstlane(lds_addr(smem + kRingOff + (j % kRingSlots) * 256)));
 }
 
-// Wave-uniform state of one workgroup's loop.
-struct MlaCtx {
-  int lane, wave, h, c32, hp, kh, t_tok, key_begin, nblk, h_half, head;
-  bool head_ok;
-};
 
-// Start of iteration t (both roles, every wave): with `compact`, the first
-// block without a valid index ends the loop there (nblk_eff = t: the P.V of
-// block t-1 still runs); the index load of block t+4; this wave's share of
-// block t+1's rows.
+// Start of iteration t (both roles, every wave): the index load of block t+4;
+// this wave's share of block t+1's rows.
+template <bool kFresh>
 __device__ __forceinline__ void iteration_start(const MlaParams& P, uint8_t* smem, const MlaCtx& c,
-                                                const DmaLanes& dl, int t, int& nblk_eff) {
-  if (P.compact && t < nblk_eff) {
-    const int32_t slot = reinterpret_cast<const int32_t*>(smem + kRingOff + (t % kRingSlots) * 256)[c.lane];
-    if (__ballot(slot_valid(P, slot)) == 0ull) nblk_eff = t;  // every wave reads the same indices
+                                                const DmaLanes& dl, int t) {
+  if (c.wave == kIdxWave && t + 4 < c.nblk) issue_index<kFresh>(P, smem, c, t + 4);
+  if (t + 1 < c.nblk) {
+    uint8_t* buf = smem + ((t + 1) % kNumBufs) * kBufBytes;
+    if (!kFresh || t + 1 < c.ncached) issue_block(smem, t + 1, dl, buf, c.wave);
+    else issue_fresh_block(smem, t + 1, buf, c.wave, c.lane);
   }
-  if (c.wave == kIdxWave && t + 4 < c.nblk) issue_index(P, smem, c.t_tok, c.key_begin, t + 4, c.lane);
-  if (t + 1 < nblk_eff) issue_block(smem, t + 1, dl, smem + ((t + 1) % kNumBufs) * kBufBytes, c.wave);
 }
 // End of iteration t: this wave's loads (block t+1's rows, index loads) have
 // landed; after the barrier every wave sees block t+1's rows and P(t).
@@ -296,6 +364,7 @@ __device__ __forceinline__ void iteration_end() {
 }
 
 // QK waves: S of block t over this wave's 32 keys, its lazy reference, P(t).
+template <bool kFresh>
 __device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, const MlaCtx& c, const DmaLanes& dl) {
   const int lane = c.lane, h = c.h, c32 = c.c32, hp = c.hp, kh = c.kh;
   // the query as the B operand over all dims: nope chunk k (64 dims), k-step j =
@@ -319,18 +388,35 @@ __device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, cons
   float m_run = -__builtin_inff();  // this key half's reference per head c32 (an integer, log2 units)
   float m_max = -__builtin_inff();  // exact running maximum (log2 units), for max_out
   float l_run = 0.f;                // sum of P against m_run, this lane's keys only
-  int nblk_eff = c.nblk;
 
-  for (int t = 0; t <= nblk_eff; ++t) {
-    iteration_start(P, smem, c, dl, t, nblk_eff);
-    if (t < nblk_eff) {
+  for (int t = 0; t <= c.nblk; ++t) {
+    iteration_start<kFresh>(P, smem, c, dl, t);
+    // a fresh block has 32 keys, all in key half 0
+    const bool fresh = kFresh && t >= c.ncached;
+    if (t < c.nblk && !(fresh && kh == 1)) {
       const uint8_t* buf = smem + (t % kNumBufs) * kBufBytes;
       const int32_t slot_t = reinterpret_cast<const int32_t*>(smem + kRingOff + (t % kRingSlots) * 256)[lane];
-      const uint64_t vmask = __ballot(slot_valid(P, slot_t));
+      const uint64_t vmask = __ballot(fresh ? fresh_valid(P, slot_t, lane) : slot_valid(P, slot_t));
       // s[r]: key 32kh + 8(r/4) + 4h + r%4, head c32
       v16f s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.f;
+      if (fresh) {
+        // bf16 rows: the key operand is read as is
+        const uint8_t* frow = buf + c32 * kFreshRowBytes;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const v4i kb = *reinterpret_cast<const v4i*>(frow + 2 * (64 * k + 32 * h + 8 * j));
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(kb), as_v8bf(qn[k][j]), s, 0, 0, 0);
+          }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const v4i rope = *reinterpret_cast<const v4i*>(frow + 2 * (512 + 16 * r + 8 * h));
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(rope), as_v8bf(qr[r]), s, 0, 0, 0);
+        }
+      } else {
       const uint8_t* row = buf + (32 * kh + c32) * kMlaRowBytes;
       const v4f ksc = *reinterpret_cast<const v4f*>(row + 512);
       const uint8_t* krow = row + 32 * h;
@@ -355,6 +441,7 @@ __device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, cons
       for (int r = 0; r < 4; ++r) {
         const v4i rope = *reinterpret_cast<const v4i*>(row + 528 + 32 * r + 16 * h);
         s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(rope), as_v8bf(qr[r]), s, 0, 0, 0);
+      }
       }
       // invalid keys score -inf (their rows are zeros); the masks are skipped
       // when every key of the block is valid, the usual case
@@ -395,6 +482,16 @@ __device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, cons
 #pragma unroll
       for (int r = 0; r < 16; ++r) lsum += pv[r];
       l_run += lsum;
+      if (fresh && !all_valid) {
+        // An invalid key's V is the zero row, so any finite P' leaves O alone.
+        // The PV waves scale a fresh block's P by adding f in [-30, 0] to the
+        // bf16 exponent field with no tile-scale term, which takes a P of 0 to
+        // -inf for f = -1 (0 * -inf = NaN): write 1.0 instead (P' = 2^f).
+        // (A cache block's term for the zero row's scale keeps 0 finite.)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (!((vb16 >> r) & 1u)) pv[r] = 1.f;
+      }
       // P as the PV A operand of k-steps 2kh, 2kh+1: lane (c32, h) holds head
       // c32, keys 16ks + 8(j/4) + 4h + j%4 (j = 0..7)
       uint8_t* pb = smem + kPOff + (t & 1) * 8192 + hp * 4 * 1024;
@@ -404,8 +501,8 @@ __device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, cons
                         cvt_pk_bf16(pv[8 * i + 4], pv[8 * i + 5]), cvt_pk_bf16(pv[8 * i + 6], pv[8 * i + 7])};
         *reinterpret_cast<v4i*>(pb + ((2 * kh + i) * 64 + lane) * 16) = pw;
       }
-      if (h == 0) ref[(((t & 1) * 2 + hp) * 2 + kh) * 32 + c32] = m_run;
     }
+    if (t < c.nblk && h == 0) ref[(((t & 1) * 2 + hp) * 2 + kh) * 32 + c32] = m_run;
     iteration_end();
   }
   // sums (both lane halves), references and maxima of this key half
@@ -420,6 +517,7 @@ __device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, cons
 }
 
 // PV waves: O += P'(t-1) . V(t-1) against R, then the normalised output.
+template <bool kFresh>
 __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, const MlaCtx& c, const DmaLanes& dl,
                                          int split) {
   const int lane = c.lane, h = c.h, c32 = c.c32, hp = c.hp, dh = c.kh;
@@ -438,17 +536,22 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
   const int e8 = m16 >> 1;
   const uint32_t vlane = (uint32_t)((8 * (e8 >> 2) + 4 * h + (e8 & 3)) * kMlaRowBytes + 256 * dh + (G & 1) * 16 +
                                     8 * (m16 & 1));
-  int nblk_eff = c.nblk;
+  // transposing bf16 reads of a fresh block: lane (G = lane/16, m = lane%16)
+  // addresses key row 4h + m/4 (+8) and dims 16(G%2) + 4(m%4) .. +3 of each
+  // 32-dim tile, and receives dim 16(G%2) + m of four consecutive keys
+  const uint32_t flane = (uint32_t)((4 * h + (m16 >> 2)) * kFreshRowBytes +
+                                    2 * (256 * dh + 16 * (G & 1) + 4 * (m16 & 3)));
 
-  for (int t = 0; t <= nblk_eff; ++t) {
-    iteration_start(P, smem, c, dl, t, nblk_eff);
+  for (int t = 0; t <= c.nblk; ++t) {
+    iteration_start<kFresh>(P, smem, c, dl, t);
     // row addresses of block t+2 (its indices landed two iterations ago); the
     // table slot was last read when block t was issued, before this iteration
-    if (c.wave == kTabWave && t + 2 < c.nblk) build_addr_table(P, smem, t + 2, lane);
+    if (c.wave == kTabWave && t + 2 < c.nblk) build_addr_table<kFresh>(P, smem, c, t + 2);
     if (t >= 1) {
       const int par = (t - 1) & 1;
       const uint8_t* bufp = smem + ((t - 1) % kNumBufs) * kBufBytes;
-      {
+      const bool fresh = kFresh && t - 1 >= c.ncached;
+      if (!fresh) {
         // exponent table of block t-1, tiles 2dh and 2dh+1 (lane = key): the
         // tile scale's exponent in the bf16 exponent field, at the PV A
         // operand position of the key (k-step key/16, lane half (key/4)%2,
@@ -523,19 +626,32 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
           eq[nxt] = *reinterpret_cast<const v4i*>(et + ((jj1 * 4 + ks1) * 2 + h) * 8);
         }
         const int k2 = ks >> 1;  // k-steps 0, 1: key half 0; 2, 3: key half 1
+        if (fresh && ks >= 2) continue;  // a fresh block's 32 keys are k-steps 0, 1
         v4i pa;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // (bit_cast of a vector element reads element 0; copy to scalars first)
-          const int pe = pq[cur][e], ee = eq[cur][e];
+          const int pe = pq[cur][e], ee = fresh ? 0 : eq[cur][e];
           const v2u16 sum = __builtin_bit_cast(v2u16, pe) + __builtin_bit_cast(v2u16, ee) +
                             __builtin_bit_cast(v2u16, fx[k2]);
           pa[e] = drop[k2] ? 0 : __builtin_bit_cast(int, sum);
         }
 #pragma unroll
-        for (int nn = 0; nn < 4; ++nn)
-          o[4 * jj + nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa), fp8x8_to_bf16(vq[cur][nn]),
-                                                                   o[4 * jj + nn], 0, 0, 0);
+        for (int nn = 0; nn < 4; ++nn) {
+          v8bf vop;
+          if (fresh) {
+            // bf16 V, no tile scale: two transposing reads give keys 4h + 0..3 and 8 + 4h + 0..3
+            uint32_t a = lds_addr(bufp) + flane + 16 * ks * kFreshRowBytes + 2 * (128 * jj + 32 * nn);
+            asm volatile("" : "+v"(a));
+            const v4s lo = lds_read_tr16_at(a);
+            const v4s hi = lds_read_tr16_at(a + 8 * kFreshRowBytes);
+            const v8s vv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            vop = __builtin_bit_cast(v8bf, vv);
+          } else {
+            vop = fp8x8_to_bf16(vq[cur][nn]);
+          }
+          o[4 * jj + nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa), vop, o[4 * jj + nn], 0, 0, 0);
+        }
       }
     }
     iteration_end();
@@ -589,6 +705,9 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
   }
 }
 
+// kFresh: a chunked prefill's token lists (cache slots, then fresh bf16 rows);
+// decode instantiates the kernel without that path.
+template <bool kFresh>
 __global__ void __launch_bounds__(kMlaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 sparse_mla_kernel(const MlaParams P) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -612,6 +731,13 @@ sparse_mla_kernel(const MlaParams P) {
   const int chunk = P.topk / P.splits;
   c.key_begin = split * chunk;
   c.nblk = chunk / kMlaKeys;
+  c.ncached = c.nblk;
+  if (kFresh) {
+    const int nc = __builtin_amdgcn_readfirstlane(P.counts[2 * c.t_tok]);
+    const int nf = __builtin_amdgcn_readfirstlane(P.counts[2 * c.t_tok + 1]);
+    c.ncached = (nc + kMlaKeys - 1) / kMlaKeys;
+    c.nblk = c.ncached + (nf + kFreshKeys - 1) / kFreshKeys;
+  }
   c.h_half = hg * kMlaHeadsPerWG + c.hp * 32;
   c.head = c.h_half + c.c32;
   c.head_ok = c.head < P.H;
@@ -619,22 +745,25 @@ sparse_mla_kernel(const MlaParams P) {
   // prologue: the indices of blocks 0-3, the address tables of blocks 0 and
   // 1, block 0's rows
   if (c.wave == kIdxWave) {
-    for (int j = 0; j < 4 && j < c.nblk; ++j) issue_index(P, smem, c.t_tok, c.key_begin, j, c.lane);
+    for (int j = 0; j < 4 && j < c.nblk; ++j) issue_index<kFresh>(P, smem, c, j);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   barrier();
   const DmaLanes dl = dma_lanes(c.wave, c.lane);
   if (c.wave == kTabWave) {
-    build_addr_table(P, smem, 0, c.lane);
-    if (c.nblk > 1) build_addr_table(P, smem, 1, c.lane);
+    if (c.nblk > 0) build_addr_table<kFresh>(P, smem, c, 0);
+    if (c.nblk > 1) build_addr_table<kFresh>(P, smem, c, 1);
   }
   barrier();
-  issue_block(smem, 0, dl, smem, c.wave);
+  if (c.nblk > 0) {
+    if (!kFresh || c.ncached > 0) issue_block(smem, 0, dl, smem, c.wave);
+    else issue_fresh_block(smem, 0, smem, c.wave, c.lane);
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   barrier();  // block 0's rows are in LDS
   // both roles run the same number of iterations and barriers
-  if (c.wave < 4) qk_waves(P, smem, c, dl);
-  else pv_waves(P, smem, c, dl, split);
+  if (c.wave < 4) qk_waves<kFresh>(P, smem, c, dl);
+  else pv_waves<kFresh>(P, smem, c, dl, split);
 }
 
 // One 64-thread workgroup per (token, head): merge the split partials.
@@ -704,7 +833,8 @@ int dsa_sparse_mla_decode(const void* q, int64_t q_token_stride, int64_t q_head_
                           void* workspace, size_t workspace_bytes, void* stream) {
   return dsa::sparse_mla_decode_impl(q, q_token_stride, q_head_stride, kv_cache, kv_block_stride_bytes,
                                      kv_block_size, kv_num_blocks, indices, idx_stride, num_tokens, num_heads, topk,
-                                     sm_scale, out, lse, num_splits, workspace, workspace_bytes, stream, nullptr, 0);
+                                     sm_scale, out, lse, num_splits, workspace, workspace_bytes, stream, nullptr,
+                                     nullptr);
 }
 
 }  // extern "C"
@@ -715,7 +845,7 @@ int sparse_mla_decode_impl(const void* q, int64_t q_token_stride, int64_t q_head
                            int64_t kv_block_stride_bytes, int kv_block_size, int64_t kv_num_blocks,
                            const int32_t* indices, int64_t idx_stride, int num_tokens, int num_heads, int topk,
                            float sm_scale, void* out, float* lse, int num_splits, void* workspace,
-                           size_t workspace_bytes, void* stream, float* max_out, int compact) {
+                           size_t workspace_bytes, void* stream, float* max_out, const MlaFresh* fresh) {
   if (num_tokens < 0 || num_heads <= 0 || (num_heads % 16) != 0)
     return set_error(kUnsupported, "sparse_mla: num_heads=%d must be a positive multiple of 16", num_heads);
   if (topk <= 0 || topk % kMlaKeys != 0)
@@ -748,8 +878,11 @@ int sparse_mla_decode_impl(const void* q, int64_t q_token_stride, int64_t q_head
 
   static int smem_status = -1;
   if (smem_status < 0) {
-    smem_status = hipFuncSetAttribute((const void*)sparse_mla_kernel,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMlaSmemBytes) == hipSuccess
+    smem_status = hipFuncSetAttribute((const void*)sparse_mla_kernel<false>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMlaSmemBytes) == hipSuccess &&
+                          hipFuncSetAttribute((const void*)sparse_mla_kernel<true>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)kMlaSmemBytes) == hipSuccess
                       ? 0 : 1;
   }
   if (smem_status) return set_error(kLaunchFailed, "sparse_mla: cannot reserve %zu B of LDS", kMlaSmemBytes);
@@ -776,15 +909,38 @@ int sparse_mla_decode_impl(const void* q, int64_t q_token_stride, int64_t q_head
   P.ws_o = nullptr;
   P.ws_lse = nullptr;
   P.max_out = num_splits == 1 ? max_out : nullptr;
-  P.compact = compact;
+  P.counts = nullptr;
+  P.fresh = nullptr;
+  P.fresh_row_stride = 0;
+  P.fresh_rows = 0;
+  P.fresh_idx = nullptr;
+  P.fresh_idx_stride = 0;
+  if (fresh) {
+    if (num_splits != 1) return set_error(kInvalidArgument, "sparse_mla: fresh rows need num_splits == 1");
+    if (!fresh->counts || (fresh->num_rows > 0 && (!fresh->rows || !fresh->idx)))
+      return set_error(kInvalidArgument, "sparse_mla: null fresh-row pointer");
+    if ((reinterpret_cast<uintptr_t>(fresh->rows) & 15) || (fresh->row_stride % 8) ||
+        (fresh->num_rows > 0 && fresh->row_stride < 576))
+      return set_error(kInvalidArgument, "sparse_mla: fresh rows must be 16-byte aligned bf16 rows of >= 576");
+    P.counts = fresh->counts;
+    P.fresh = static_cast<const uint16_t*>(fresh->rows);
+    P.fresh_row_stride = fresh->row_stride;
+    P.fresh_rows = fresh->num_rows;
+    P.fresh_idx = fresh->idx;
+    P.fresh_idx_stride = fresh->idx_stride;
+  }
   if (num_splits > 1) {
     const size_t rows = (size_t)num_splits * num_tokens * num_heads;
     P.ws_o = static_cast<float*>(workspace);
     P.ws_lse = P.ws_o + rows * kMlaDv;
   }
   const int64_t nwg = (int64_t)num_tokens * P.head_groups * num_splits;
-  hipLaunchKernelGGL(sparse_mla_kernel, dim3((unsigned)nwg), dim3(kMlaThreads), kMlaSmemBytes,
-                     (hipStream_t)stream, P);
+  if (fresh)
+    hipLaunchKernelGGL(sparse_mla_kernel<true>, dim3((unsigned)nwg), dim3(kMlaThreads), kMlaSmemBytes,
+                       (hipStream_t)stream, P);
+  else
+    hipLaunchKernelGGL(sparse_mla_kernel<false>, dim3((unsigned)nwg), dim3(kMlaThreads), kMlaSmemBytes,
+                       (hipStream_t)stream, P);
   if (int rc = check_launch("dsa_sparse_mla_decode")) return rc;
   if (num_splits > 1) {
     hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3((unsigned)(num_tokens * num_heads)), dim3(64), 0,

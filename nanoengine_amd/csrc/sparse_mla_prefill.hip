@@ -82,8 +82,6 @@ struct PrParams {
   uint16_t* out;
   float* max_logits;
   float* lse;
-  int compact;  // the valid indices of a row come first: stop at the first block with none
-  int merge;    // combine with the (out, lse, max_logits) already stored for these rows
 };
 
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
@@ -167,11 +165,6 @@ sparse_mla_prefill_kernel(const PrParams P) {
   const int h_half = hg * kPrHeadsPerWG + hp * 32;
   const int head = h_half + c32;
   const bool head_ok = head < P.H;
-  // merging a compacted list that is empty leaves the stored result as it is
-  if (P.compact && P.merge) {
-    const int32_t first = P.idx[(int64_t)t * P.idx_stride];
-    if (first < 0 || (int64_t)first >= P.s_kv) return;
-  }
 
   // query B operands: k-step ks of the nope quarter = dims 128q + 16ks + 8h .. +8,
   // rope = dims 512 + 16q + 8h .. +8, of head c32
@@ -217,8 +210,6 @@ sparse_mla_prefill_kernel(const PrParams P) {
     const uint8_t* buf = smem + (n % kPrNumBufs) * kPrBufBytes;
     const int32_t slot_n = reinterpret_cast<const int32_t*>(smem + kPrRingOff + (n % kPrRingSlots) * 128)[c32];
     const uint32_t vmask = (uint32_t)__ballot(slot_n >= 0 && (int64_t)slot_n < P.s_kv);
-    // every wave reads the same indices, so all of them leave at the same block
-    if (P.compact && vmask == 0u) break;
     if (wave == kIdxWave && n + 4 < nblk) issue_index(P, smem, t, n + 4, lane);
 
     // ---- partial S^T[32 keys x 32 heads]: s[r] = key 8(r/4) + 4h + r%4, head c32.
@@ -328,13 +319,6 @@ sparse_mla_prefill_kernel(const PrParams P) {
   }
 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // merge mode: this row's earlier result, read by every wave before the
-  // barriers below, after which one lane per head overwrites it
-  float lse_prev = -__builtin_inff(), max_prev = -__builtin_inff();
-  if (P.merge && head_ok) {
-    lse_prev = P.lse[(int64_t)t * P.H + head];
-    max_prev = P.max_logits[(int64_t)t * P.H + head];
-  }
   l_run += shfl_xor(l_run, 32);
   barrier();
   if (h == 0) mx[q4] = l_run;
@@ -346,39 +330,17 @@ sparse_mla_prefill_kernel(const PrParams P) {
   if (h_half >= P.H) return;
   const bool any = l_run > 0.f;
   const float inv = any ? 1.f / l_run : 0.f;
-  float lse_new = any ? (m_run + __builtin_amdgcn_logf(l_run)) * kLn2 : -__builtin_inff();
-  float max_new = any ? m_max * kLn2 : -__builtin_inff();
-  // weights of the earlier and of this result (merge_attention_states' LSE rule)
-  float w_prev = 0.f, w_this = 1.f;
-  if (P.merge) {
-    const float m = fmaxf(lse_prev, lse_new);
-    if (m == -__builtin_inff()) {
-      w_prev = 0.f;
-      w_this = 0.f;
-    } else {
-      const float a = __expf(lse_prev - m), b = __expf(lse_new - m);
-      w_prev = a / (a + b);
-      w_this = b / (a + b);
-      lse_new = m + __logf(a + b);
-    }
-    max_new = fmaxf(max_new, max_prev);
-  }
+  const float lse_new = any ? (m_run + __builtin_amdgcn_logf(l_run)) * kLn2 : -__builtin_inff();
+  const float max_new = any ? m_max * kLn2 : -__builtin_inff();
   // o[nt][r]: head h_half + 8(r/4) + 4h + r%4, dim 128 q4 + 32nt + c32
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
-    const float ir = __shfl(inv * w_this, hr, 64);
-    const float wp = __shfl(w_prev, hr, 64);
+    const float ir = __shfl(inv, hr, 64);
     if (h_half + hr < P.H) {
       uint16_t* orow = P.out + ((int64_t)t * P.H + h_half + hr) * kPrDv + 128 * q4 + c32;
-      if (P.merge) {
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          orow[32 * nt] = (uint16_t)f32_to_bf16_rne(fmaf(wp, bf16_to_f32(orow[32 * nt]), o[nt][r] * ir));
-      } else {
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
-      }
+      for (int nt = 0; nt < 4; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
     }
   }
   if (h == 0 && q4 == 0 && head_ok) {
@@ -392,13 +354,14 @@ sparse_mla_prefill_kernel(const PrParams P) {
 // i = g - cu_k[b] is cached row i of sequence b while i < k_len - q_len (its
 // physical slot block_table[b][i / bs] * bs + i % bs in the paged fp8 cache),
 // else fresh row cu_q[b] + i - (k_len - q_len). Each token's two lists are
-// compacted in index order and padded with -1 to their widths. One 256-thread
-// workgroup per token.
+// compacted in index order and padded with -1 to their widths, and their
+// lengths go to counts[2t], counts[2t+1]. One 256-thread workgroup per token.
 __global__ void __launch_bounds__(256)
 prefill_split_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int topk, const void* __restrict__ cu_q,
                      const void* __restrict__ cu_k, int cu_is_64, int num_seqs, int64_t total_k,
                      const int32_t* __restrict__ bt, int64_t bt_stride, int block_size,
-                     int32_t* __restrict__ cached, int cached_w, int32_t* __restrict__ fresh, int fresh_w) {
+                     int32_t* __restrict__ cached, int cached_w, int32_t* __restrict__ fresh, int fresh_w,
+                     int32_t* __restrict__ counts) {
   auto cu = [&](const void* p, int i) -> int64_t {
     return cu_is_64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
   };
@@ -453,6 +416,10 @@ prefill_split_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int to
     __syncthreads();
   }
   const int nc = s_base[0], nf = s_base[1];
+  if (tid == 0) {
+    counts[2 * t] = nc;
+    counts[2 * t + 1] = nf;
+  }
   for (int e = nc + tid; e < cached_w; e += 256) crow[e] = -1;
   for (int e = nf + tid; e < fresh_w; e += 256) frow[e] = -1;
 }
@@ -462,7 +429,7 @@ prefill_split_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int to
 static int sparse_mla_prefill_impl(const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* kv,
                                    int64_t kv_row_stride, int64_t s_kv, const int32_t* indices, int64_t idx_stride,
                                    int num_tokens, int num_heads, int topk, float sm_scale, void* out,
-                                   float* max_logits, float* lse, void* stream, int compact, int merge);
+                                   float* max_logits, float* lse, void* stream);
 }  // namespace dsa
 
 extern "C" {
@@ -473,7 +440,7 @@ int dsa_sparse_mla_prefill(const void* q, int64_t q_token_stride, int64_t q_head
                            float* lse, void* stream) {
   return dsa::sparse_mla_prefill_impl(q, q_token_stride, q_head_stride, kv, kv_row_stride, s_kv, indices,
                                       idx_stride, num_tokens, num_heads, topk, sm_scale, out, max_logits, lse,
-                                      stream, 0, 0);
+                                      stream);
 }
 
 }  // extern "C"
@@ -483,7 +450,7 @@ namespace dsa {
 static int sparse_mla_prefill_impl(const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* kv,
                                    int64_t kv_row_stride, int64_t s_kv, const int32_t* indices, int64_t idx_stride,
                                    int num_tokens, int num_heads, int topk, float sm_scale, void* out,
-                                   float* max_logits, float* lse, void* stream, int compact, int merge) {
+                                   float* max_logits, float* lse, void* stream) {
   if (num_tokens < 0 || num_heads <= 0 || (num_heads % 16) != 0)
     return set_error(kUnsupported, "sparse_mla_prefill: num_heads=%d must be a positive multiple of 16", num_heads);
   if (topk <= 0 || topk % kPrKeys != 0)
@@ -520,8 +487,6 @@ static int sparse_mla_prefill_impl(const void* q, int64_t q_token_stride, int64_
   P.out = static_cast<uint16_t*>(out);
   P.max_logits = max_logits;
   P.lse = lse;
-  P.compact = compact;
-  P.merge = merge;
   const int64_t nwg = (int64_t)num_tokens * P.head_groups;
   if (nwg > INT32_MAX) return set_error(kInvalidArgument, "sparse_mla_prefill: grid too large");
   hipLaunchKernelGGL(sparse_mla_prefill_kernel, dim3((unsigned)nwg), dim3(kPrThreads), kPrSmemBytes,
@@ -531,7 +496,7 @@ static int sparse_mla_prefill_impl(const void* q, int64_t q_token_stride, int64_
 
 static inline size_t pf_align(size_t x) { return (x + 255) & ~(size_t)255; }
 static inline int cached_width(int topk) { return (topk + 63) / 64 * 64; }
-static inline int fresh_width(int topk) { return (topk + kPrKeys - 1) / kPrKeys * kPrKeys; }
+static inline int fresh_width(int topk) { return (topk + 31) / 32 * 32; }
 
 }  // namespace dsa
 
@@ -540,7 +505,8 @@ extern "C" {
 size_t dsa_sparse_mla_prefill_paged_workspace_bytes(int num_tokens, int topk) {
   using namespace dsa;
   if (num_tokens <= 0 || topk <= 0) return 0;
-  return pf_align((size_t)num_tokens * cached_width(topk) * 4) + pf_align((size_t)num_tokens * fresh_width(topk) * 4);
+  return pf_align((size_t)num_tokens * cached_width(topk) * 4) + pf_align((size_t)num_tokens * fresh_width(topk) * 4) +
+         pf_align((size_t)num_tokens * 2 * 4);
 }
 
 int dsa_sparse_mla_prefill_paged(const void* q, int64_t q_token_stride, int64_t q_head_stride,
@@ -564,20 +530,20 @@ int dsa_sparse_mla_prefill_paged(const void* q, int64_t q_token_stride, int64_t 
   int32_t* cached = static_cast<int32_t*>(workspace);
   int32_t* fresh_idx =
       reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + pf_align((size_t)num_tokens * cw * 4));
+  int32_t* counts = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + pf_align((size_t)num_tokens * cw * 4) +
+                                               pf_align((size_t)num_tokens * fw * 4));
   hipStream_t st = (hipStream_t)stream;
-  // 1. each token's indices split into cache slots and fresh rows, compacted
+  // 1. each token's indices split into cache slots and fresh rows, compacted and counted
   hipLaunchKernelGGL(prefill_split_kernel, dim3((unsigned)num_tokens), dim3(256), 0, st, indices, idx_stride, topk,
                      cu_seqlens_q, cu_seqlens_k, cu_is_64, num_seqs, total_k, block_table, bt_stride, kv_block_size,
-                     cached, cw, fresh_idx, fw);
+                     cached, cw, fresh_idx, fw, counts);
   if (int rc = check_launch("dsa_sparse_mla_prefill_paged(split)")) return rc;
-  // 2. the cached keys straight from the paged fp8 cache, exact dequantisation in registers
-  if (int rc = sparse_mla_decode_impl(q, q_token_stride, q_head_stride, kv_cache, kv_block_stride_bytes, kv_block_size,
-                                      kv_num_blocks, cached, cw, num_tokens, num_heads, cw, sm_scale, out, lse, 1,
-                                      nullptr, 0, stream, max_logits, 1))
-    return rc;
-  // 3. the fresh bf16 rows, merged into that result by LSE
-  return sparse_mla_prefill_impl(q, q_token_stride, q_head_stride, fresh, fresh_row_stride, total_q, fresh_idx, fw,
-                                 num_tokens, num_heads, fw, sm_scale, out, max_logits, lse, stream, 1, 1);
+  // 2. the decode kernel over each token's cache slots (fp8 rows, exact
+  // dequantisation in registers) followed by its fresh bf16 rows, one softmax
+  const MlaFresh fr{counts, fresh, fresh_row_stride, total_q, fresh_idx, fw};
+  return sparse_mla_decode_impl(q, q_token_stride, q_head_stride, kv_cache, kv_block_stride_bytes, kv_block_size,
+                                kv_num_blocks, cached, cw, num_tokens, num_heads, cw, sm_scale, out, lse, 1, nullptr, 0,
+                                stream, max_logits, &fr);
 }
 
 }  // extern "C"

@@ -102,7 +102,8 @@ def test_prefill_entry_points_reject_bad_arguments(lib):
     assert lib.dsa_mla_prefill_kv(P, 42640, 64, P, 0, P, P, 0, 1, 10, P, 512, P, 576, P) == 1
     assert lib.dsa_mla_prefill_kv(P, 42640, 64, P, 0, P, P, 0, 1, 0, P, 576, P, 576, P) == 0   # nothing to do
     # paged sparse prefill: workspace sizing and the workspace check come before any launch
-    assert lib.dsa_sparse_mla_prefill_paged_workspace_bytes(8192, 2048) == 2 * 8192 * 2048 * 4
+    # cache-slot and fresh-row lists, 2048 wide each, and two counts per token
+    assert lib.dsa_sparse_mla_prefill_paged_workspace_bytes(8192, 2048) == 2 * 8192 * 2048 * 4 + 8192 * 8
     assert lib.dsa_sparse_mla_prefill_paged_workspace_bytes(0, 2048) == 0
     ws = lib.dsa_sparse_mla_prefill_paged_workspace_bytes(10, 2048)
     f = ctypes.c_float(0.1)
