@@ -74,11 +74,13 @@ def _paged_case(cuda, seed=7, H=128, topk=256):
 
 
 def test_paged_prefill_matches_assembled_rows(cuda):
-    """The paged sparse prefill (cached keys from the fp8 cache through the
-    decode kernel, fresh keys as bf16 rows, LSE merge) against the assembled
-    bf16 keys through the bf16 prefill kernel and against the oracle; the
-    sequences include one with no cached prefix, a token with no valid index
-    and indices past the key count."""
+    """The paged sparse prefill (one decode-kernel pass per token: its cached
+    keys from the fp8 cache, then its fresh keys as bf16 rows in 32-row blocks)
+    against the assembled bf16 keys through the bf16 prefill kernel and against
+    the oracle. The sequences include one with no cached prefix (up to 129
+    fresh keys per token: five fresh blocks, the last partly invalid), a token
+    with no valid index and indices past the key count. A NaN row here has
+    meant an invalid fresh key's P scaled to -inf (0 * -inf)."""
     print("paged sparse prefill", flush=True)
     q, kv, bt, cu_q, cu_k, fresh, idx, total_k, host = _paged_case(cuda)
     scale = 192 ** -0.5
@@ -86,8 +88,8 @@ def test_paged_prefill_matches_assembled_rows(cuda):
     asm = mla_utils.assemble_prefill_kv(kv, bt, cu_q, cu_k, fresh.unsqueeze(1), total_k)[:, 0]
     eo, emx, else_ = ops.sparse_mla_prefill(q, asm, idx, scale)
     torch.cuda.synchronize()
-    # two GPU results, each rounded to bf16 on its own (the paged one also rounds
-    # the cached part before the merge): a bf16 ulp of the value on top of atol
+    # two GPU results, each rounded to bf16 on its own, with different summation
+    # orders: a bf16 ulp of the value on top of atol
     assert torch.all((o.float() - eo.float()).abs() <= 2e-2 + eo.float().abs() * 2.0 ** -7)
     fin = torch.isfinite(else_)
     assert torch.equal(torch.isfinite(lse), fin) and torch.equal(torch.isfinite(mx), torch.isfinite(emx))
