@@ -142,3 +142,16 @@ def test_fused_prefill_topk_rejects_bad_arguments(lib):
     assert lib.dsa_mqa_topk(*bad, ws, P) == 1
     bad = list(args); bad[7] = 0                                           # nothing to do
     assert lib.dsa_mqa_topk(*bad, 0, P) == 0
+
+
+def test_microbenchmark_library_exports_its_probes():
+    """The measurements behind the kernels' design (bench.py --micro) come from
+    a separate library; it loads without a device and exports every probe."""
+    from nanoengine_amd.build import MICROBENCH_LIB
+    if not MICROBENCH_LIB.exists():
+        from nanoengine_amd import build
+        build.build()
+    mb = ctypes.CDLL(str(MICROBENCH_LIB))
+    for name in ["dsa_mb_page_read", "dsa_mb_row_gather", "dsa_mb_lds_read", "dsa_mb_valu_issue",
+                 "dsa_mb_mfma_rate", "dsa_mb_fp8_mfma_sum"]:
+        assert hasattr(mb, name), name
