@@ -168,7 +168,20 @@ def micro():
         peak = FP8_PEAK_TFLOPS if "fp8" in name else BF16_PEAK_TFLOPS
         print(json.dumps({"micro": "mfma_rate", "shape": name, "TFLOPs": round(total / t / 1e12, 1),
                           "frac_of_peak": round(total / t / 1e12 / peak, 3)}), flush=True)
-    # 6. summation precision of the scaled fp8 MFMA: products 2^p and +-1.875 in one output
+    # 6. MFMA beside VALU on one SIMD: cycles per iteration (4 MFMAs / 16 VALU) of each kind of wave
+    mcyc = torch.zeros(256 * 8, dtype=torch.int64, device=dev)
+    for op, name in ((0, "v_fma_f32"), (1, "v_cvt_scalef32_pk_bf16_fp8")):
+        res = {"micro": "mfma_beside_valu", "valu_op": name}
+        for mode, tag in ((1, "mfma_alone"), (2, "valu_alone"), (3, "both")):
+            iters = 2000
+            check(lib.dsa_mb_mix(op, mode, iters, 256, ctypes.c_void_p(fsink.data_ptr()),
+                                 ctypes.c_void_p(mcyc.data_ptr()), st), "mix")
+            torch.cuda.synchronize()
+            c = mcyc.view(256, 8).double()
+            res[tag] = {"mfma_wave": round(float(c[:, :4].mean()) / iters, 1) if mode & 1 else None,
+                        "valu_wave": round(float(c[:, 4:].mean()) / iters, 1) if mode & 2 else None}
+        print(json.dumps(res), flush=True)
+    # 7. summation precision of the scaled fp8 MFMA: products 2^p and +-1.875 in one output
     out = torch.zeros(17 * 64, dtype=torch.float32, device=dev)
     for sign in (1, -1):
         check(lib.dsa_mb_fp8_mfma_sum(sign, ctypes.c_void_p(out.data_ptr()), st), "fp8_mfma_sum")
