@@ -92,9 +92,11 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 // P' = P * 2^(e + m_kh - R) is formed by adding to the bf16 exponent field,
 // which needs P' to stay a normal number: P of a valid key is kept at or above
-// 2^-30 of its key half's reference, and a key half more than 2^30 below the
-// other is left out of that block's P.V (its share is below 2^-22 of the
-// row's). With tile scales above 2^-66, P' stays above 2^-126.
+// 2^-30 of its key half's reference, and a key half whose reference is more
+// than 2^30 below R is scaled by 2^-30 instead of 2^(m_kh - R). Each of its
+// keys then adds at most 2^-22 of R's scale where it should add less, the
+// same bound as leaving the half out. With tile scales above 2^-66, P' stays
+// above 2^-126.
 constexpr float kMinLogP = -30.0f;
 constexpr int kDropExp = -30;
 constexpr int kIdxWave = 7;                // the wave that fetches the row indices
@@ -581,14 +583,14 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
           for (int r = 0; r < 16; ++r) o[nt][r] *= ar[r];
       }
       // per key half: m_kh - R (<= 0) for the bf16 exponent field, or left out
+      // (a key half with no valid key yet has only zero rows in this block, so
+      // any finite P' is fine there; a half more than 2^30 below R is scaled
+      // by 2^-30 instead of 2^f, which keeps P' a normal number)
       int fx[2];
-      bool drop[2];
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         const float mk = k2 == 0 ? m0 : m1;
-        const bool none = mk == -__builtin_inff();  // no valid key in this half yet: its P are 0
-        const int f = none ? 0 : (int)(mk - R);
-        drop[k2] = none || f < kDropExp;
+        const int f = mk == -__builtin_inff() ? 0 : max((int)(mk - R), kDropExp);
         fx[k2] = (f << 7) & 0xffff;
         fx[k2] |= fx[k2] << 16;
       }
@@ -634,7 +636,7 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
           const int pe = pq[cur][e], ee = fresh ? 0 : eq[cur][e];
           const v2u16 sum = __builtin_bit_cast(v2u16, pe) + __builtin_bit_cast(v2u16, ee) +
                             __builtin_bit_cast(v2u16, fx[k2]);
-          pa[e] = drop[k2] ? 0 : __builtin_bit_cast(int, sum);
+          pa[e] = __builtin_bit_cast(int, sum);
         }
 #pragma unroll
         for (int nn = 0; nn < 4; ++nn) {

@@ -81,6 +81,38 @@ def test_large_score_jumps_redo_blocks(cuda, splits):
     _check(o, lse, eo, elv, lse_atol=1e-3 / 192 ** -0.5)
 
 
+def test_key_half_far_below_the_other(cuda):
+    """Each 64-key block holds the token's best keys in its first 32 slots and
+    its worst in the last 32 (ordered by head 0's score, softmax scale 1), so
+    the second key half's reference falls more than 2^30 below the first's:
+    P.V scales that half by 2^-30 instead of its true, smaller factor (which
+    keeps the bf16 exponent arithmetic normal) and the output must still match
+    the oracle."""
+    T, H, K = 2, 128, 2048
+    q, kv, idx = _case(T, H, K, num_blocks=80, seed=23)
+    scale = 1.0
+    rows = kv.reshape(-1, 656).cpu().numpy()
+    deq = O.dequant_mla_rows(rows).astype(np.float64)
+    qf = q.float().cpu().numpy().astype(np.float64)
+    ih = idx.cpu().numpy()
+    for t in range(T):
+        order = np.argsort(-(deq[ih[t]] @ qf[t, 0]))          # best first, by head 0
+        best, worst = ih[t][order[:K // 2]], ih[t][order[K // 2:]][::-1]
+        ih[t] = np.stack([best.reshape(-1, 32), worst.reshape(-1, 32)], 1).reshape(-1)
+    idx = torch.from_numpy(ih).to(cuda)
+    # precondition: for head 0, some block's second-half reference (running
+    # maximum, log2 units) is more than 30 below the first half's
+    sc = np.einsum("td,tkd->tk", qf[:, 0], deq[ih]) * scale / np.log(2.0)
+    halves = sc.reshape(T, K // 64, 2, 32).max(-1)
+    run = np.maximum.accumulate(halves, axis=1)
+    assert np.any(run[:, :, 0] - run[:, :, 1] > 30.0)
+    print("mla key halves far apart", flush=True)
+    o, lse = ops.sparse_mla_decode(q, kv, idx, scale, num_splits=1)
+    torch.cuda.synchronize()
+    eo, elv = _oracle(q, kv, idx, scale)
+    _check(o, lse, eo, elv, lse_atol=1e-3 / 192 ** -0.5)
+
+
 def test_invalid_indices_and_empty_rows(cuda):
     q, kv, idx = _case(3, 128, 1024, num_blocks=40, seed=3, invalid_frac=0.3)
     idx[1] = -1                         # a query with no valid index: o = 0, lse = -inf
