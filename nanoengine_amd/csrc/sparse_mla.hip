@@ -99,7 +99,7 @@ constexpr float kRescaleThreshold = 8.0f;  // log2 units
 // above 2^-126.
 constexpr float kMinLogP = -30.0f;
 constexpr int kDropExp = -30;
-constexpr int kIdxWave = 7;                // the wave that fetches the row indices
+constexpr int kIdxWave = 3;                // the wave that fetches the row indices (a QK wave)
 
 static_assert(kBufBytes % 1024 == 0, "a block of rows must be whole wave-wide loads");
 static_assert(kMlaSmemBytes <= 160 * 1024, "LDS budget");
@@ -208,7 +208,7 @@ __device__ __forceinline__ v8i lds_read32(const uint8_t* p) {
 // wave-wide loads, lane l of load i taking 16-byte piece c = 64(first + i) + l
 // of the packed block: row c / 41, byte 16 (c % 41) of it. Those (row, byte)
 // pairs are loop invariants, computed once per lane (DmaLanes).
-constexpr int kTabWave = 6;  // the wave that builds the row-address table
+constexpr int kTabWave = 2;  // the wave that builds the row-address table (a QK wave: the PV waves' chain is longer)
 
 // Wave-uniform state of one workgroup's loop. Blocks [0, ncached) are 64 cache
 // slots each, blocks [ncached, nblk) 32 fresh bf16 rows each.
@@ -393,6 +393,9 @@ __device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, cons
 
   for (int t = 0; t <= c.nblk; ++t) {
     iteration_start<kFresh>(P, smem, c, dl, t);
+    // row addresses of block t+2 (its indices landed two iterations ago); the
+    // table slot was last read when block t was issued, before this iteration
+    if (c.wave == kTabWave && t + 2 < c.nblk) build_addr_table<kFresh>(P, smem, c, t + 2);
     // a fresh block has 32 keys, all in key half 0
     const bool fresh = kFresh && t >= c.ncached;
     if (t < c.nblk && !(fresh && kh == 1)) {
@@ -546,9 +549,6 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
 
   for (int t = 0; t <= c.nblk; ++t) {
     iteration_start<kFresh>(P, smem, c, dl, t);
-    // row addresses of block t+2 (its indices landed two iterations ago); the
-    // table slot was last read when block t was issued, before this iteration
-    if (c.wave == kTabWave && t + 2 < c.nblk) build_addr_table<kFresh>(P, smem, c, t + 2);
     if (t >= 1) {
       const int par = (t - 1) & 1;
       const uint8_t* bufp = smem + ((t - 1) % kNumBufs) * kBufBytes;
