@@ -32,18 +32,6 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Two OCP e4m3fn bytes (selected by `hi`: bytes 0-1 or 2-3 of w) -> two floats.
-__device__ __forceinline__ v2f fp8x2_to_f32(uint32_t w, bool hi) {
-  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true)
-            : __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-}
-
-// Pack the bf16 truncations of two floats (lo in bits 0-15). Exact for values
-// that are already bf16-representable, such as fp8 times a power of two.
-__device__ __forceinline__ uint32_t pack_bf16_trunc(float lo, float hi) {
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-
 // Round-to-nearest-even float -> bf16 bits.
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float x) {
   uint32_t u = __float_as_uint(x);
@@ -79,19 +67,6 @@ __device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, floa
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-
-// Dequantise 16 fp8 bytes (v4i) times `scale` into 16 bf16 (two v4i: dims
-// 0-7 and 8-15), one v_cvt_scalef32_pk_bf16_fp8 per pair of values. Exact for
-// power-of-two scales (an e4m3 value times 2^k is a bf16 value).
-__device__ __forceinline__ void dequant16_fp8_bf16(v4i raw, float scale, v4i& lo, v4i& hi) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const int p0 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[w], scale, false));
-    const int p1 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[w], scale, true));
-    if (w < 2) { lo[2 * w] = p0; lo[2 * w + 1] = p1; }
-    else       { hi[2 * (w - 2)] = p0; hi[2 * (w - 2) + 1] = p1; }
-  }
-}
 
 // Per-row candidate list of the exact top-k (device workspace): a score
 // threshold t_key (order key), the number of candidates appended, a flag set

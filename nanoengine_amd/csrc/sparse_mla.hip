@@ -163,11 +163,6 @@ __device__ __forceinline__ int cvt_pk_bf16(float a, float b) {
   return __builtin_bit_cast(int, __builtin_convertvector(x, v2bf));
 }
 
-__device__ __forceinline__ v2i lds_read_tr8(const uint8_t* p) {
-  typedef __attribute__((address_space(3))) v2i lds_v2i;
-  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)p);
-}
-
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
