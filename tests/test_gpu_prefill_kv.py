@@ -108,3 +108,22 @@ def test_paged_prefill_matches_assembled_rows(cuda):
     assert np.abs(lse[sample].cpu().numpy()[ofin] - olse[ofin]).max() <= 1e-3
     assert np.abs(mx[sample].cpu().numpy()[ofin] - omx[ofin]).max() <= 1e-3
     assert torch.all(o[int(cu_q_h[3]) + 1] == 0)
+
+
+def test_flash_mla_sparse_fwd_paged_adapter(cuda):
+    """The reference-shaped entry (indices [s_q, 1, topk], key_states
+    [total_q, 1, 576], int64 cu_seqlens) gives the same result as the op."""
+    from nanoengine_amd import flash_mla
+    print("flash_mla_sparse_fwd_paged adapter", flush=True)
+    q, kv, bt, cu_q, cu_k, fresh, idx, total_k, _ = _paged_case(cuda, seed=11)
+    scale = 192 ** -0.5
+    o, mx, lse = ops.sparse_mla_prefill_paged(q, kv, bt, cu_q, cu_k, fresh, idx, scale, total_k)
+    o2, mx2, lse2 = flash_mla.flash_mla_sparse_fwd_paged(q, kv, bt, cu_q.to(torch.int64), cu_k.to(torch.int64),
+                                                         fresh.unsqueeze(1), idx.unsqueeze(1).to(torch.int64),
+                                                         scale)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2)
+    assert torch.equal(torch.nan_to_num(lse, neginf=-1e30), torch.nan_to_num(lse2, neginf=-1e30))
+    assert torch.equal(torch.nan_to_num(mx, neginf=-1e30), torch.nan_to_num(mx2, neginf=-1e30))
+    with pytest.raises(ValueError):
+        flash_mla.flash_mla_sparse_fwd_paged(q, kv, bt, cu_q, cu_k, fresh, idx, scale)   # indices not [s_q, 1, topk]
