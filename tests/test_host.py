@@ -100,3 +100,27 @@ def test_fused_step_rejects_non_indexer_page_size():
     from nanoengine_amd.pipeline import DsaDecodeStep
     with pytest.raises(ValueError, match="page_size 64"):
         DsaDecodeStep(2, 1, 4096, page_size=32, device="cpu", fused=True)
+
+
+def test_merge_attention_states_equals_one_softmax():
+    """Two halves of one key set, each with its own softmax output and LSE,
+    merged by LSE equal the softmax over all keys (mla_utils.py:12-23); an
+    empty half (LSE -inf) leaves the other unchanged."""
+    from nanoengine_amd import mla_utils
+    g = torch.Generator().manual_seed(0)
+    T, H, D, N = 3, 4, 16, 40
+    s = torch.randn(T, H, N, generator=g, dtype=torch.float64) * 4
+    v = torch.randn(T, N, D, generator=g, dtype=torch.float64)
+
+    def part(sl):
+        p = torch.softmax(s[..., sl], -1)
+        return torch.einsum("thn,tnd->thd", p, v[:, sl]), torch.logsumexp(s[..., sl], -1).transpose(0, 1)
+
+    lo, llse = part(slice(0, 13))
+    hi, hlse = part(slice(13, N))
+    full, flse = part(slice(0, N))
+    merged, mlse = mla_utils.merge_attention_states(lo, llse, hi, hlse)
+    assert torch.allclose(merged, full, atol=1e-12) and torch.allclose(mlse, flse, atol=1e-12)
+    empty = torch.full_like(hlse, -float("inf"))
+    same, slse = mla_utils.merge_attention_states(lo, llse, torch.zeros_like(hi), empty)
+    assert torch.allclose(same, lo, atol=1e-12) and torch.equal(slse, llse)
