@@ -517,30 +517,35 @@ __device__ __forceinline__ void qk_waves(const MlaParams& P, uint8_t* smem, cons
 }
 
 // PV waves: O += P'(t-1) . V(t-1) against R, then the normalised output.
+// Wave dq = w - 4 owns O[64 heads x dims 128dq .. 128dq+127], exactly V tile
+// dq, as two head tiles (the head halves): each V byte is converted once per
+// workgroup, and one exponent per key scales both tiles' P.
 template <bool kFresh>
 __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, const MlaCtx& c, const DmaLanes& dl,
                                          int split) {
-  const int lane = c.lane, h = c.h, c32 = c.c32, hp = c.hp, dh = c.kh;
+  const int lane = c.lane, h = c.h, c32 = c.c32, dq = c.wave - 4;
   const float* ref = reinterpret_cast<const float*>(smem + kRefOff);
-  // this wave's exponent table (its two V tiles 2dh, 2dh+1): [2][4 k-steps][2 h][8 u16]
-  uint16_t* et = reinterpret_cast<uint16_t*>(smem + kEOff) + (c.wave - 4) * 256;
-  v16f o[8];  // o[nt][r]: head h_half + 8(r/4) + 4h + r%4, dim 256dh + 32nt + c32
+  // this wave's exponent table (V tile dq): [4 k-steps][2 h][8 u16]
+  uint16_t* et = reinterpret_cast<uint16_t*>(smem + kEOff) + dq * 256;
+  v16f o[2][4];  // o[mt][nn][r]: head 32mt + 8(r/4) + 4h + r%4 of the workgroup, dim 128dq + 32nn + c32
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
-  float R = -__builtin_inff();  // reference of O per head c32 (an integer, log2 units)
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[mt][i][r] = 0.f;
+  float R[2] = {-__builtin_inff(), -__builtin_inff()};  // reference of O per head tile, head c32 (log2 units)
   // transposing V reads: lane (G = lane/16, m = lane%16) addresses key row
   // 8(e/4) + 4h + e%4 (e = m/2) and dims (G%2)*16 + 8(m%2) of each 32-dim tile
   const int m16 = lane & 15, G = lane >> 4;
   const int e8 = m16 >> 1;
-  const uint32_t vlane = (uint32_t)((8 * (e8 >> 2) + 4 * h + (e8 & 3)) * kMlaRowBytes + 256 * dh + (G & 1) * 16 +
+  const uint32_t vlane = (uint32_t)((8 * (e8 >> 2) + 4 * h + (e8 & 3)) * kMlaRowBytes + 128 * dq + (G & 1) * 16 +
                                     8 * (m16 & 1));
   // transposing bf16 reads of a fresh block: lane (G = lane/16, m = lane%16)
   // addresses key row 4h + m/4 (+8) and dims 16(G%2) + 4(m%4) .. +3 of each
   // 32-dim tile, and receives dim 16(G%2) + m of four consecutive keys
   const uint32_t flane = (uint32_t)((4 * h + (m16 >> 2)) * kFreshRowBytes +
-                                    2 * (256 * dh + 16 * (G & 1) + 4 * (m16 & 3)));
+                                    2 * (128 * dq + 16 * (G & 1) + 4 * (m16 & 3)));
 
   for (int t = 0; t <= c.nblk; ++t) {
     iteration_start<kFresh>(P, smem, c, dl, t);
@@ -549,96 +554,101 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
       const uint8_t* bufp = smem + ((t - 1) % kNumBufs) * kBufBytes;
       const bool fresh = kFresh && t - 1 >= c.ncached;
       if (!fresh) {
-        // exponent table of block t-1, tiles 2dh and 2dh+1 (lane = key): the
-        // tile scale's exponent in the bf16 exponent field, at the PV A
-        // operand position of the key (k-step key/16, lane half (key/4)%2,
-        // element 4((key/8)%2) + key%4)
+        // exponent table of block t-1, tile dq (lane = key): the tile scale's
+        // exponent in the bf16 exponent field, at the PV A operand position of
+        // the key (k-step key/16, lane half (key/4)%2, element 4((key/8)%2) + key%4)
         const int key = lane;
-        const uint2 sb = *reinterpret_cast<const uint2*>(bufp + key * kMlaRowBytes + 512 + 8 * dh);
+        const uint32_t sb = *reinterpret_cast<const uint32_t*>(bufp + key * kMlaRowBytes + 512 + 4 * dq);
         const int pos = ((key >> 4) * 2 + ((key >> 2) & 1)) * 8 + 4 * ((key >> 3) & 1) + (key & 3);
-        et[pos] = (uint16_t)((uint32_t)((((int)((sb.x >> 23) & 0xffu)) - 127) << 7) & 0xffffu);
-        et[64 + pos] = (uint16_t)((uint32_t)((((int)((sb.y >> 23) & 0xffu)) - 127) << 7) & 0xffffu);
+        et[pos] = (uint16_t)((uint32_t)((((int)((sb >> 23) & 0xffu)) - 127) << 7) & 0xffffu);
       }
-      // O's reference follows the larger key-half reference; O moves by a power of two
-      const float m0 = ref[((par * 2 + hp) * 2 + 0) * 32 + c32];
-      const float m1 = ref[((par * 2 + hp) * 2 + 1) * 32 + c32];
-      const float mn = fmaxf(m0, m1);
-      const bool up = mn > R;
-      if (__ballot(up)) {
-        const float alpha = up ? __builtin_amdgcn_exp2f(R - mn) : 1.f;  // 0 from -inf
-        R = up ? mn : R;
-        int hb = 4 * h;
-        asm volatile("" : "+v"(hb));
-        float ar[16];
+      // each head tile's O follows the larger of its key-half references; O
+      // moves by a power of two
+      int fx[2][2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ar[r] = __shfl(alpha, 8 * (r >> 2) + hb + (r & 3), 64);
+      for (int mt = 0; mt < 2; ++mt) {
+        const float m0 = ref[((par * 2 + mt) * 2 + 0) * 32 + c32];
+        const float m1 = ref[((par * 2 + mt) * 2 + 1) * 32 + c32];
+        const float mn = fmaxf(m0, m1);
+        const bool up = mn > R[mt];
+        if (__ballot(up)) {
+          const float alpha = up ? __builtin_amdgcn_exp2f(R[mt] - mn) : 1.f;  // 0 from -inf
+          R[mt] = up ? mn : R[mt];
+          int hb = 4 * h;
+          asm volatile("" : "+v"(hb));
+          float ar[16];
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt)
+          for (int r = 0; r < 16; ++r) ar[r] = __shfl(alpha, 8 * (r >> 2) + hb + (r & 3), 64);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o[nt][r] *= ar[r];
+          for (int nn = 0; nn < 4; ++nn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[mt][nn][r] *= ar[r];
+        }
+        // per key half: m_kh - R (<= 0) for the bf16 exponent field (a key half
+        // with no valid key yet has only zero rows in this block, so any finite
+        // P' is fine there; a half more than 2^30 below R is scaled by 2^-30
+        // instead of 2^f, which keeps P' a normal number)
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const float mk = k2 == 0 ? m0 : m1;
+          const int f = mk == -__builtin_inff() ? 0 : max((int)(mk - R[mt]), kDropExp);
+          fx[mt][k2] = (f << 7) & 0xffff;
+          fx[mt][k2] |= fx[mt][k2] << 16;
+        }
       }
-      // per key half: m_kh - R (<= 0) for the bf16 exponent field, or left out
-      // (a key half with no valid key yet has only zero rows in this block, so
-      // any finite P' is fine there; a half more than 2^30 below R is scaled
-      // by 2^-30 instead of 2^f, which keeps P' a normal number)
-      int fx[2];
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const float mk = k2 == 0 ? m0 : m1;
-        const int f = mk == -__builtin_inff() ? 0 : max((int)(mk - R), kDropExp);
-        fx[k2] = (f << 7) & 0xffff;
-        fx[k2] |= fx[k2] << 16;
-      }
-      const uint8_t* pb = smem + kPOff + par * 8192 + hp * 4 * 1024;
+      const uint8_t* pb = smem + kPOff + par * 8192;
       const uint32_t vb = lds_addr(bufp) + vlane;
       // The transposing reads take no immediate offset, so each address is
       // formed from an opaque base right before use; otherwise all of them
       // would be hoisted out of the loop into registers.
-      auto vaddr = [&](int it) {
-        uint32_t a = vb + (16 * (it >> 1)) * kMlaRowBytes + 128 * (it & 1);
+      auto vaddr = [&](int ks) {
+        uint32_t a = vb + (16 * ks) * kMlaRowBytes;
         asm volatile("" : "+v"(a));
         return a;
       };
-      // iteration it = (k-step ks = it/2, tile 2dh + it%2): its P, exponent
-      // and V reads issued one iteration ahead
+      // k-step ks: its P (both head tiles), exponent and V reads issued one
+      // k-step ahead
       v2i vq[2][4];
-      v4i pq[2], eq[2];
+      v4i pq[2][2], eq[2];
       {
         const uint32_t a0 = vaddr(0);
 #pragma unroll
         for (int nn = 0; nn < 4; ++nn) vq[0][nn] = lds_read_tr8_at(a0 + 32 * nn);
-        pq[0] = *reinterpret_cast<const v4i*>(pb + lane * 16);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) pq[0][mt] = *reinterpret_cast<const v4i*>(pb + mt * 4096 + lane * 16);
         eq[0] = *reinterpret_cast<const v4i*>(et + h * 8);
       }
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int ks = it >> 1, jj = it & 1;
-        const int cur = it & 1, nxt = cur ^ 1;
-        if (it + 1 < 8) {
-          const int ks1 = (it + 1) >> 1, jj1 = (it + 1) & 1;
-          const uint32_t a1 = vaddr(it + 1);
+      for (int ks = 0; ks < 4; ++ks) {
+        const int cur = ks & 1, nxt = cur ^ 1;
+        if (ks + 1 < 4) {
+          const uint32_t a1 = vaddr(ks + 1);
 #pragma unroll
           for (int nn = 0; nn < 4; ++nn) vq[nxt][nn] = lds_read_tr8_at(a1 + 32 * nn);
-          pq[nxt] = *reinterpret_cast<const v4i*>(pb + (ks1 * 64 + lane) * 16);
-          eq[nxt] = *reinterpret_cast<const v4i*>(et + ((jj1 * 4 + ks1) * 2 + h) * 8);
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+            pq[nxt][mt] = *reinterpret_cast<const v4i*>(pb + mt * 4096 + ((ks + 1) * 64 + lane) * 16);
+          eq[nxt] = *reinterpret_cast<const v4i*>(et + ((ks + 1) * 2 + h) * 8);
         }
         const int k2 = ks >> 1;  // k-steps 0, 1: key half 0; 2, 3: key half 1
         if (fresh && ks >= 2) continue;  // a fresh block's 32 keys are k-steps 0, 1
-        v4i pa;
+        v4i pa[2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // (bit_cast of a vector element reads element 0; copy to scalars first)
-          const int pe = pq[cur][e], ee = fresh ? 0 : eq[cur][e];
-          const v2u16 sum = __builtin_bit_cast(v2u16, pe) + __builtin_bit_cast(v2u16, ee) +
-                            __builtin_bit_cast(v2u16, fx[k2]);
-          pa[e] = __builtin_bit_cast(int, sum);
-        }
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            // (bit_cast of a vector element reads element 0; copy to scalars first)
+            const int pe = pq[cur][mt][e], ee = fresh ? 0 : eq[cur][e];
+            const v2u16 sum = __builtin_bit_cast(v2u16, pe) + __builtin_bit_cast(v2u16, ee) +
+                              __builtin_bit_cast(v2u16, fx[mt][k2]);
+            pa[mt][e] = __builtin_bit_cast(int, sum);
+          }
 #pragma unroll
         for (int nn = 0; nn < 4; ++nn) {
           v8bf vop;
           if (fresh) {
             // bf16 V, no tile scale: two transposing reads give keys 4h + 0..3 and 8 + 4h + 0..3
-            uint32_t a = lds_addr(bufp) + flane + 16 * ks * kFreshRowBytes + 2 * (128 * jj + 32 * nn);
+            uint32_t a = lds_addr(bufp) + flane + 16 * ks * kFreshRowBytes + 2 * (32 * nn);
             asm volatile("" : "+v"(a));
             const v4s lo = lds_read_tr16_at(a);
             const v4s hi = lds_read_tr16_at(a + 8 * kFreshRowBytes);
@@ -647,7 +657,9 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
           } else {
             vop = fp8x8_to_bf16(vq[cur][nn]);
           }
-          o[4 * jj + nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa), vop, o[4 * jj + nn], 0, 0, 0);
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+            o[mt][nn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_v8bf(pa[mt]), vop, o[mt][nn], 0, 0, 0);
         }
       }
     }
@@ -655,50 +667,56 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
   }
   barrier();  // the QK waves' sums, references and maxima are in LDS
   const float* fin = reinterpret_cast<const float*>(smem + kFinOff);
-  // total of P per head c32 against R, and the exact maximum
-  float lt = 0.f, mm = -__builtin_inff();
-#pragma unroll
-  for (int k2 = 0; k2 < 2; ++k2) {
-    const float lk = fin[(hp * 2 + k2) * 32 + c32];
-    const float mk = fin[128 + (hp * 2 + k2) * 32 + c32];
-    if (mk != -__builtin_inff()) lt += lk * __builtin_amdgcn_exp2f(mk - R);
-    mm = fmaxf(mm, fin[256 + (hp * 2 + k2) * 32 + c32]);
-  }
-  const bool any = lt > 0.f;
-  const float inv = any ? 1.f / lt : 0.f;
-  const float lse = any ? (R + __builtin_amdgcn_logf(lt)) * kLn2 : -__builtin_inff();
-  const int h_half = c.h_half;
-  if (h_half >= P.H) return;
+  const int hg_base = c.h_half - c.hp * 32;  // the workgroup's first head
   int hb = 4 * h;
   asm volatile("" : "+v"(hb));
-  if (P.splits == 1) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
-      const float ir = __shfl(inv, 8 * (r >> 2) + hb + (r & 3), 64);
-      if (h_half + hr < P.H) {
-        uint16_t* orow = P.out + ((int64_t)c.t_tok * P.H + h_half + hr) * kMlaDv + 256 * dh + c32;
+  for (int mt = 0; mt < 2; ++mt) {
+    // total of P per head c32 of tile mt against R, and the exact maximum
+    float lt = 0.f, mm = -__builtin_inff();
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) orow[32 * nt] = (uint16_t)f32_to_bf16_rne(o[nt][r] * ir);
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const float lk = fin[(mt * 2 + k2) * 32 + c32];
+      const float mk = fin[128 + (mt * 2 + k2) * 32 + c32];
+      if (mk != -__builtin_inff()) lt += lk * __builtin_amdgcn_exp2f(mk - R[mt]);
+      mm = fmaxf(mm, fin[256 + (mt * 2 + k2) * 32 + c32]);
+    }
+    const bool any = lt > 0.f;
+    const float inv = any ? 1.f / lt : 0.f;
+    const float lse = any ? (R[mt] + __builtin_amdgcn_logf(lt)) * kLn2 : -__builtin_inff();
+    const int h_half = hg_base + 32 * mt;
+    if (h_half >= P.H) continue;
+    const int head = h_half + c32;
+    const bool head_ok = head < P.H;
+    if (P.splits == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
+        const float ir = __shfl(inv, 8 * (r >> 2) + hb + (r & 3), 64);
+        if (h_half + hr < P.H) {
+          uint16_t* orow = P.out + ((int64_t)c.t_tok * P.H + h_half + hr) * kMlaDv + 128 * dq + c32;
+#pragma unroll
+          for (int nn = 0; nn < 4; ++nn) orow[32 * nn] = (uint16_t)f32_to_bf16_rne(o[mt][nn][r] * ir);
+        }
       }
-    }
-    if (dh == 0 && h == 0 && c.head_ok) {
-      if (P.lse) P.lse[(int64_t)c.t_tok * P.H + c.head] = lse;
-      if (P.max_out) P.max_out[(int64_t)c.t_tok * P.H + c.head] = any ? mm * kLn2 : -__builtin_inff();
-    }
-  } else {
-    const int64_t row0 = ((int64_t)split * P.T + c.t_tok) * P.H + h_half;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
-      const float ir = __shfl(inv, 8 * (r >> 2) + hb + (r & 3), 64);
-      if (h_half + hr < P.H) {
-        float* orow = P.ws_o + (row0 + hr) * kMlaDv + 256 * dh + c32;
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) orow[32 * nt] = o[nt][r] * ir;
+      if (dq == 0 && h == 0 && head_ok) {
+        if (P.lse) P.lse[(int64_t)c.t_tok * P.H + head] = lse;
+        if (P.max_out) P.max_out[(int64_t)c.t_tok * P.H + head] = any ? mm * kLn2 : -__builtin_inff();
       }
+    } else {
+      const int64_t row0 = ((int64_t)split * P.T + c.t_tok) * P.H + h_half;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int hr = 8 * (r >> 2) + 4 * h + (r & 3);
+        const float ir = __shfl(inv, 8 * (r >> 2) + hb + (r & 3), 64);
+        if (h_half + hr < P.H) {
+          float* orow = P.ws_o + (row0 + hr) * kMlaDv + 128 * dq + c32;
+#pragma unroll
+          for (int nn = 0; nn < 4; ++nn) orow[32 * nn] = o[mt][nn][r] * ir;
+        }
+      }
+      if (dq == 0 && h == 0 && head_ok) P.ws_lse[row0 + c32] = lse;
     }
-    if (dh == 0 && h == 0 && c.head_ok) P.ws_lse[row0 + c32] = lse;
   }
 }
 
