@@ -22,10 +22,11 @@
 //            below the largest one.) Then the wave's own online softmax over
 //            its 32 keys: a lazy reference m (an integer, log2 units) per
 //            head, P = 2^(s - m) to LDS as bf16, the reference beside it.
-//   PV waves 4-7: wave (hp, dh) owns O[32 heads of hp x dims 256dh .. +256]
-//            and adds the previous block's P.V: the two key halves' P come
-//            with their own references m0, m1; the wave keeps O against
-//            R = max(m0, m1) (rescaling O by a power of two when R moves) and
+//   PV waves 4-7: wave dq owns O[all 64 heads x dims 128dq .. +128] (V
+//            tile dq, two head tiles) and adds the previous block's P.V: the
+//            two key halves' P come with their own references m0, m1; per head
+//            tile the wave keeps O against R = max(m0, m1) (rescaling by a
+//            power of two when R moves) and
 //            forms P' = P * 2^(e + m_kh - R), e the tile scale exponent of
 //            each key, by adding to the bf16 exponent field; V is read from
 //            the raw rows with ds_read_b64_tr_b8 (8 keys x 1 dim per lane, the
