@@ -367,8 +367,8 @@ DSA_API int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, i
 /* Sparse MLA prefill straight from the paged fp8 MLA cache: the keys a token
  * selects from its sequence's cached prefix are read as 656-byte rows through
  * the block table and dequantised exactly in registers (the decode kernel);
- * only the keys it selects among the chunk's fresh rows are read as bf16.
- * The two partial results are merged by LSE.
+ * only the keys it selects among the chunk's fresh rows are read as bf16, in
+ * the same kernel pass and under the same softmax.
  *   q, indices, num_tokens, num_heads, topk, sm_scale, out, max_logits, lse:
  *              as dsa_sparse_mla_prefill, with indices into the ragged key
  *              order of total_k = cu_k[-1] keys (sequence b's keys at cu_k[b] ..)
