@@ -7,7 +7,10 @@ filter's contiguous per-wave page ranges and the XCDs) checked against the CPU
 oracle: logits within 1e-3 relative, logical top-2048 bit-exact against the
 exact selection over the GPU logits (and tie-only differences against the
 oracle's float64 logits), physical slots bit-exact, MLA o within atol 2e-2 and
-LSE within 1e-3."""
+LSE within 1e-3.
+
+Config 0 (B=4, 1K-4K tokens) runs the same step with every row checked, for
+seeds 0, 1 and 2; configs 1 and 3 are checked at their own shapes too."""
 import numpy as np
 import pytest
 import torch
@@ -108,3 +111,40 @@ def test_config1_mla_alone_sampled_tokens_match_oracle(cuda):
                                      192 ** -0.5)
         assert np.abs(o[r].float().cpu().numpy() - eo[0]).max() <= 2e-2
         assert np.abs(lse[r].cpu().numpy() - el[0]).max() <= 1e-3
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_config0_full_step_every_row_matches_oracle(cuda, seed):
+    """BASELINE config 0 through the fused decode step: B=4 sequences of 1024,
+    2048, 3000 and 4096 tokens (two rows at or below 2048 keep every position,
+    two go through the exact top-2048), 128 MLA heads, seeds 0, 1 and 2 as the
+    measurement plan asks. Every row is checked against the oracle to the same
+    bounds as config 2."""
+    B, H, K = 4, 128, 2048
+    lens = [1024, 2048, 3000, 4096]
+    print(f"config0 B={B} lens={lens} H={H} K={K} seed={seed}", flush=True)
+    inp = synth.make_indexer_inputs(lens, next_n=1, seed=seed, device=cuda)
+    kv = synth.make_mla_cache(int(inp.block_tables.max().item()) + 1, seed=seed, device=cuda)
+    q_mla = synth.make_mla_query(B, H, seed=seed, device=cuda)
+    max_ctx = inp.block_tables.shape[1] * 64
+    step = DsaDecodeStep(B, 1, max_ctx, num_heads=H, index_topk=K, device=cuda)
+    seq = step.expand_lens(inp.context_lens)
+    o, lse, logical, physical = step(inp.q_fp8, inp.weights, inp.cache, seq, inp.block_tables, inp.block_tables,
+                                     q_mla, kv, 192 ** -0.5)
+    logits = ops.indexer_logits(inp.q_fp8.view(B, 1, 64, 128), inp.cache, inp.weights, seq.view(B, 1),
+                                inp.block_tables, max_ctx)
+    torch.cuda.synchronize()
+    rows = np.arange(B)
+    data = SC.sample_from_device(rows, q_idx_fp8=inp.q_fp8, weights=inp.weights, cache=inp.cache, lens=lens,
+                                 block_tables=inp.block_tables, q_mla=q_mla, kv=kv, logits=logits,
+                                 logical=logical, physical=physical, o=o, lse=lse)
+    rep = SC.check_step_rows(**data, sm_scale=192 ** -0.5, topk=K)
+    print(rep, flush=True)
+    assert rep["ok"], rep
+    lg = logical.cpu().numpy()
+    for r, L in enumerate(lens):
+        if L <= K:
+            # a row no longer than k keeps every position, in order, then -1
+            assert np.array_equal(lg[r, :L], np.arange(L)) and np.all(lg[r, L:] == -1)
+        else:
+            assert np.all((lg[r] >= 0) & (lg[r] < L)) and len(np.unique(lg[r])) == K
