@@ -337,3 +337,18 @@ def test_step_check_catches_wrong_outputs():
     o2 = o.copy()
     o2[1, 2, 3] += 0.05
     assert not SC.check_step_rows(**dict(base, gpu_o=o2))["ok"]
+
+
+def test_step_check_logits_scale_for_cancelling_rows():
+    """A row of one or two keys whose head sum cancels has no usable RMS: its
+    logits are measured against a tenth of their magnitude sum
+    sum_h |w_h| relu(q_h . k) s. An f32-sized error passes, a 1e-3 one fails."""
+    from oracle import step_check as SC
+    e = np.array([[1e-9, 0.0]], np.float32)
+    ctx = np.array([1])
+    mag = np.array([[1.0, 0.0]], np.float32)
+    g = e + np.array([[1e-7, 0.0]], np.float32)
+    assert SC.check_logits(g, e, ctx) > SC.LOGITS_RTOL
+    assert SC.check_logits(g, e, ctx, mag) <= SC.LOGITS_RTOL
+    g2 = e + np.array([[1e-3, 0.0]], np.float32)
+    assert SC.check_logits(g2, e, ctx, mag) > SC.LOGITS_RTOL
