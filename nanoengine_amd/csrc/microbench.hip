@@ -16,6 +16,10 @@
 //                  product 2^p and one product +-1.875 in the same output: the
 //                  exact sum is 2^p +- 1.875; the instruction's result shows
 //                  how far below the largest product the sum keeps bits.
+//   mfma_probe     one MFMA (scaled fp8 16x16x128 / 32x32x64, fp8 16x16x32 /
+//                  32x32x16, bf16 32x32x16) per wave on operands the host
+//                  builds, so that the host can compare each dot with its
+//                  exact sum.
 //
 // Each entry returns 0 or a HIP error code; timing is done by the caller with
 // events around the launch, except where a kernel reports clock64 cycles.
@@ -227,6 +231,59 @@ __global__ void __launch_bounds__(64) fp8_mfma_sum_kernel(int sign, float* __res
   }
 }
 
+
+// MFMA summation probe over arbitrary operands: workgroup c (one wave) loads
+// its operand registers from a[c][lane][8] and b[c][lane][8] (ints; each shape
+// uses the leading bytes its operand needs) and stores every result register
+// to out[c][lane][16]. SHAPE 0: scaled 16x16x128 fp8 (unit scales); 1: scaled
+// 32x32x64 fp8; 2: v_mfma_f32_16x16x32_fp8_fp8; 3: v_mfma_f32_32x32x16_fp8_fp8;
+// 4: v_mfma_f32_32x32x16_bf16. The host builds the operands in each shape's
+// lane layout and compares the result with the exact sum of the products.
+template <int SHAPE>
+__global__ void __launch_bounds__(64) mfma_probe_kernel(const int* __restrict__ a, const int* __restrict__ b,
+                                                        float* __restrict__ out) {
+  const int lane = threadIdx.x;
+  const int64_t base = ((int64_t)blockIdx.x * 64 + lane) * 8;
+  v8i A, B;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    A[i] = a[base + i];
+    B[i] = b[base + i];
+  }
+  float r[16];
+  if constexpr (SHAPE == 0) {
+    const v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0,
+                                                                   127);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = i < 4 ? c[i] : 0.f;
+  } else if constexpr (SHAPE == 1) {
+    const v16f c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, (v16f){}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = c[i];
+  } else if constexpr (SHAPE == 2) {
+    const long la = ((long)(unsigned)A[1] << 32) | (unsigned)A[0];
+    const long lb = ((long)(unsigned)B[1] << 32) | (unsigned)B[0];
+    const v4f c = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(la, lb, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = i < 4 ? c[i] : 0.f;
+  } else if constexpr (SHAPE == 3) {
+    const long la = ((long)(unsigned)A[1] << 32) | (unsigned)A[0];
+    const long lb = ((long)(unsigned)B[1] << 32) | (unsigned)B[0];
+    const v16f c = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(la, lb, (v16f){}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = c[i];
+  } else {
+    const v4i a4 = {A[0], A[1], A[2], A[3]}, b4 = {B[0], B[1], B[2], B[3]};
+    const v16f c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a4), __builtin_bit_cast(v8bf, b4),
+                                                          (v16f){}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = c[i];
+  }
+  float* o = out + ((int64_t)blockIdx.x * 64 + lane) * 16;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = r[i];
+}
+
 // MFMA beside VALU on one SIMD: a workgroup of 8 waves puts waves w and w + 4
 // on SIMD w. Waves 0-3 run 4 independent 32x32x16 bf16 MFMA chains when
 // (mode & 1); waves 4-7 run 16 independent v_fma_f32 (OP 0) or
@@ -345,6 +402,19 @@ MB_API int dsa_mb_mix(int op, int mode, int iters, int grid, float* sink, unsign
 
 MB_API int dsa_mb_fp8_mfma_sum(int sign, float* out, void* stream) {
   hipLaunchKernelGGL(fp8_mfma_sum_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, sign, out);
+  return (int)hipGetLastError();
+}
+
+MB_API int dsa_mb_mfma_probe(int shape, int cases, const int* a, const int* b, float* out, void* stream) {
+  if (cases <= 0) return 0;
+  switch (shape) {
+    case 0: hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(cases), dim3(64), 0, (hipStream_t)stream, a, b, out); break;
+    case 1: hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(cases), dim3(64), 0, (hipStream_t)stream, a, b, out); break;
+    case 2: hipLaunchKernelGGL(mfma_probe_kernel<2>, dim3(cases), dim3(64), 0, (hipStream_t)stream, a, b, out); break;
+    case 3: hipLaunchKernelGGL(mfma_probe_kernel<3>, dim3(cases), dim3(64), 0, (hipStream_t)stream, a, b, out); break;
+    case 4: hipLaunchKernelGGL(mfma_probe_kernel<4>, dim3(cases), dim3(64), 0, (hipStream_t)stream, a, b, out); break;
+    default: return 1;
+  }
   return (int)hipGetLastError();
 }
 

@@ -104,3 +104,34 @@ def test_fp8_mqa_logits_entry_point(cuda):
     got = got.cpu().numpy()
     _check_windows(got, exp, ks, ke)
     assert np.array_equal(np.isneginf(got), np.isneginf(exp))
+
+
+def test_mqa_logits_within_the_derived_mfma_bound(cuda):
+    """Queries whose head sums cancel over 48 wide-range fp8 keys (see
+    test_gpu_indexer.py's cancelling rows) through the ragged prefill logits
+    kernel (32x32x64 scaled fp8 MFMA): every logit within 1e-3 relative or
+    within the derived MFMA bound (oracle ``indexer_logit_error_bound``)."""
+    from oracle import step_check as SC
+    from test_gpu_indexer import _wide_cancelling
+    rng = np.random.default_rng(11)
+    N, M, H = 48, 3, 64
+    qs, ws = [], []
+    k = None
+    for _ in range(M):
+        q, k_, w = _wide_cancelling(np.random.default_rng(rng.integers(1 << 30)), N, H)
+        k = k_ if k is None else k
+        # the keys are shared: re-project this query's weights on the first keys
+        d = O.fp8_e4m3fn_decode(k).astype(np.float64) @ O.fp8_e4m3fn_decode(q).astype(np.float64).T
+        R = np.maximum(d, 0.0)
+        w = (w - np.linalg.pinv(R) @ (R @ w)).astype(np.float32)
+        qs.append(q)
+        ws.append(w)
+    q, w = np.stack(qs), np.stack(ws)
+    sc = np.full(N, 2.0 ** -6, np.float32)
+    ks, ke = np.zeros(M, np.int32), np.full(M, N, np.int32)
+    got = _run(cuda, q, k, sc, w, ks, ke, True)
+    exp = O.mqa_logits(q, k, sc, w, ks, ke, clean_logits=True)
+    rep = SC.check_logits(got, exp, ke, SC.ragged_logit_bound(q, w, k, sc))
+    print(rep, flush=True)
+    assert rep["over_rtol"] > 0, rep
+    assert rep["ok"], rep

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 EDGES = [1, 2, 63, 64, 65, 511, 512, 513, 2047, 2048, 2049, 4095, 4096, 4097]
 
 
-@pytest.mark.parametrize("case", range(16))
+@pytest.mark.parametrize("case", range(24))
 def test_random_step_every_row_matches_oracle(cuda, case):
     rng = np.random.default_rng(1000 + case)
     B = int(rng.integers(1, 10))

@@ -332,23 +332,82 @@ def test_step_check_catches_wrong_outputs():
     lg2[0] = np.sort(lg2[0])
     assert not SC.check_step_rows(**dict(base, gpu_logical=lg2))["ok"]
     lgt = logits.copy()
-    lgt[1, 5] *= 1.01
+    lgt[1, 5] *= 1.1
     assert not SC.check_step_rows(**dict(base, gpu_logits=lgt))["ok"]
     o2 = o.copy()
     o2[1, 2, 3] += 0.05
     assert not SC.check_step_rows(**dict(base, gpu_o=o2))["ok"]
 
 
-def test_step_check_logits_scale_for_cancelling_rows():
-    """A row of one or two keys whose head sum cancels has no usable RMS: its
-    logits are measured against a tenth of their magnitude sum
-    sum_h |w_h| relu(q_h . k) s. An f32-sized error passes, a 1e-3 one fails."""
+def _cancelling_row(seed):
+    """A query token, 8 keys and head weights whose weighted head sums all
+    cancel: w lies in the null space of relu(q_h . k_t) [8 x 64], so every
+    logit sum_h w_h relu(q_h . k_t) is ~0 and the row has no RMS scale."""
+    rng = np.random.default_rng(seed)
+    q = O.fp8_e4m3fn_encode(np.clip(rng.standard_normal((64, 128)) * 60, -440, 440))
+    k = O.fp8_e4m3fn_encode(np.clip(rng.standard_normal((8, 128)) * 60, -440, 440))
+    s = np.full(8, 2.0 ** -10, np.float32)
+    qf, kf = O.fp8_e4m3fn_decode(q).astype(np.float64), O.fp8_e4m3fn_decode(k).astype(np.float64)
+    d = kf @ qf.T                                              # [8, 64]
+    R = np.maximum(d, 0.0)
+    w = rng.standard_normal(64) * 64 ** -0.5 * 2.0 ** -9
+    w = w - np.linalg.pinv(R) @ (R @ w)                        # project onto the null space of R
+    return q, k, s, w.astype(np.float32), qf, kf, d
+
+
+def test_mfma_logit_bound_accepts_truncated_sums_and_rejects_wrong_head_sums():
+    """The derived bound of the scaled fp8 MFMA (indexer_logit_error_bound) on
+    a row whose head sums all cancel, where 1e-3 relative has no scale:
+    * the exact logits are ~0 and the bound is a small share (< 5%) of the
+      logit's magnitude sum sum_h |w_h| relu(q_h . k) s, so it is not vacuous;
+    * sums whose products are truncated toward zero at 2^-13 of the largest
+      product (the behaviour the GPU probe measures) pass check_logits;
+    * a wrong head sum fails it: one head dropped, |w| for w, no ReLU, the
+      weights shifted by one head, the key scale left out."""
     from oracle import step_check as SC
-    e = np.array([[1e-9, 0.0]], np.float32)
-    ctx = np.array([1])
-    mag = np.array([[1.0, 0.0]], np.float32)
-    g = e + np.array([[1e-7, 0.0]], np.float32)
-    assert SC.check_logits(g, e, ctx) > SC.LOGITS_RTOL
-    assert SC.check_logits(g, e, ctx, mag) <= SC.LOGITS_RTOL
-    g2 = e + np.array([[1e-3, 0.0]], np.float32)
-    assert SC.check_logits(g2, e, ctx, mag) > SC.LOGITS_RTOL
+    for seed in range(3):
+        q, k, s, w, qf, kf, d = _cancelling_row(seed)
+        wd = w.astype(np.float64)
+        exact = (np.maximum(d, 0.0) @ wd) * s
+        mag = (np.maximum(d, 0.0) @ np.abs(wd)) * s
+        assert np.all(np.abs(exact) < 1e-6 * mag)
+        B = O.indexer_logit_error_bound(q, w, k, s)
+        assert np.all(B > 0) and np.all(B < 5e-2 * mag), (B / mag)
+        # products truncated toward zero at 2^(E-13): within the bound
+        P = kf[:, None, :] * qf[None, :, :]
+        quantum = np.exp2(np.floor(np.log2(np.abs(P).max(-1))) - 13)[..., None]
+        dt = (np.trunc(P / quantum) * quantum).sum(-1)
+        trunc_logit = ((np.maximum(dt, 0.0) @ wd) * s)[None, :]
+        ctx = np.array([8])
+        bound = SC.ragged_logit_bound(q[None], w[None], k, s)
+        rep = SC.check_logits(trunc_logit.astype(np.float32), exact[None].astype(np.float32), ctx, bound)
+        assert rep["ok"] and rep["over_rtol"] == 8, rep
+        hot = int(np.argmax(np.abs(wd) * np.maximum(d, 0.0).sum(0)))   # a head that contributes
+        wrong = {
+            "dropped head": (np.maximum(np.delete(d, hot, axis=1), 0.0) @ np.delete(wd, hot)) * s,
+            "abs weights": (np.maximum(d, 0.0) @ np.abs(wd)) * s,
+            "no relu": (d @ wd) * s,
+            "shifted weights": (np.maximum(d, 0.0) @ np.roll(wd, 1)) * s,
+        }
+        for name, val in wrong.items():
+            rep = SC.check_logits(val[None].astype(np.float32), exact[None].astype(np.float32), ctx, bound)
+            assert not rep["ok"], (name, rep)
+
+
+def test_mfma_dot_bound_two_product_probe():
+    """fp8_dot_error_bound on the two-product probe 2^p + 1.875 (one output of
+    the scaled MFMA): the GPU keeps 1.875 exactly to p = 10, then 1.75, 1.5,
+    1.0, then nothing (bench.py --micro, fp8_mfma_sum); the bound's remainder
+    term equals each observed loss exactly (the bound adds one quantum for
+    the one addition and one f32 rounding)."""
+    kept = {11: 1.75, 12: 1.5, 13: 1.0, 14: 0.0, 15: 0.0, 16: 0.0}
+    for p in range(17):
+        a = min(p, 8)
+        q = np.zeros((1, 128)); k = np.zeros((1, 128))
+        q[0, 0], k[0, 0] = 2.0 ** a, 2.0 ** (p - a)
+        q[0, 1], k[0, 1] = 1.875, 1.0
+        dots, bnd = O.fp8_dot_error_bound(q, k)
+        lost = 1.875 - kept.get(p, 1.875)
+        assert dots[0, 0] == 2.0 ** p + 1.875
+        quantum = 2.0 ** (p - O.MFMA_FP8_BITS)
+        assert bnd[0, 0] - O.F32_EPS * dots[0, 0] - quantum == pytest.approx(lost, abs=1e-12), p
