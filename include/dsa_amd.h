@@ -373,7 +373,10 @@ DSA_API int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, i
  *              as dsa_sparse_mla_prefill, with indices into the ragged key
  *              order of total_k = cu_k[-1] keys (sequence b's keys at cu_k[b] ..)
  *   kv_cache   [blocks, kv_block_size, 656] bytes (block stride, block count)
- *   block_table [num_seqs, M] int32; cu_seqlens_q/_k [num_seqs + 1] int32
+ *   block_table [num_seqs, bt_width] int32 (row stride bt_stride); a cached
+ *              key whose column is past bt_width, or whose block is negative
+ *              or >= kv_num_blocks, is skipped like an index of -1
+ *   cu_seqlens_q/_k [num_seqs + 1] int32
  *              (cu_is_64 = 0) or int64: key i of sequence b is cached row i
  *              while i < k_len - q_len, else fresh row cu_q[b] + i - (k_len - q_len)
  *   fresh      [total_q, 576] bf16 (row stride fresh_row_stride elements)
@@ -390,7 +393,7 @@ DSA_API size_t dsa_sparse_mla_prefill_paged_workspace_bytes(int num_tokens, int 
 DSA_API int dsa_sparse_mla_prefill_paged(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                                          const uint8_t* kv_cache, int64_t kv_block_stride_bytes,
                                          int kv_block_size, int64_t kv_num_blocks,
-                                         const int32_t* block_table, int64_t bt_stride,
+                                         const int32_t* block_table, int64_t bt_stride, int bt_width,
                                          const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64,
                                          int num_seqs, int64_t total_k, const void* fresh,
                                          int64_t fresh_row_stride, int64_t total_q, const int32_t* indices,
@@ -419,8 +422,10 @@ DSA_API int dsa_prefill_windows(const void* cu_seqlens_q, const void* cu_seqlens
 
 /* The sparse prefill's ragged bf16 keys [total_k, 576] from the paged fp8
  * MLA cache (656-byte rows) and the chunk's fresh rows.
- *   kv_cache   [blocks, block_size, 656] bytes, block stride kv_block_stride_bytes
- *   block_table [num_seqs, M] int32 (row stride bt_stride)
+ *   kv_cache   [kv_num_blocks, block_size, 656] bytes, block stride kv_block_stride_bytes
+ *   block_table [num_seqs, bt_width] int32 (row stride bt_stride); a cached row
+ *              whose column is past bt_width, or whose block is negative or
+ *              >= kv_num_blocks, is written as zeros
  *   cu_seqlens_q/_k [num_seqs + 1] int32 (cu_is_64 = 0) or int64; sequence b's
  *              fresh queries are the last q_len of its k_len keys
  *   fresh      [cu_q[-1], 576] bf16 rows (row stride fresh_row_stride elements)
@@ -433,7 +438,8 @@ DSA_API int dsa_prefill_windows(const void* cu_seqlens_q, const void* cu_seqlens
  * mla_utils.py:118-236, kernel/triton/hopper/fp8_utils.py:153-196) as called at
  * dlengine/runtime/models/deepseek_v2/deepseek_v2.py:1573-1604. */
 DSA_API int dsa_mla_prefill_kv(const uint8_t* kv_cache, int64_t kv_block_stride_bytes,
-                               int kv_block_size, const int32_t* block_table, int64_t bt_stride,
+                               int kv_block_size, int64_t kv_num_blocks, const int32_t* block_table,
+                               int64_t bt_stride, int bt_width,
                                const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64,
                                int num_seqs, int64_t total_k, const void* fresh,
                                int64_t fresh_row_stride, void* out, int64_t out_row_stride,

@@ -53,11 +53,11 @@ SIGNATURES = {
     "dsa_gather_indexer_cache": (c_int, [_P, c_int64, c_int, c_int, _P, c_int64, _P, c_int, c_int, c_int64, _P, _P,
                                          _P]),
     "dsa_sparse_mla_prefill_paged_workspace_bytes": (c_size_t, [c_int, c_int]),
-    "dsa_sparse_mla_prefill_paged": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int, c_int64, _P, c_int64, _P, _P,
-                                             c_int, c_int, c_int64, _P, c_int64, c_int64, _P, c_int64, c_int, c_int,
+    "dsa_sparse_mla_prefill_paged": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int, c_int64, _P, c_int64, c_int,
+                                             _P, _P, c_int, c_int, c_int64, _P, c_int64, c_int64, _P, c_int64, c_int, c_int,
                                              c_int, c_float, _P, _P, _P, _P, c_size_t, _P]),
-    "dsa_mla_prefill_kv": (c_int, [_P, c_int64, c_int, _P, c_int64, _P, _P, c_int, c_int, c_int64, _P, c_int64, _P,
-                                   c_int64, _P]),
+    "dsa_mla_prefill_kv": (c_int, [_P, c_int64, c_int, c_int64, _P, c_int64, c_int, _P, _P, c_int, c_int, c_int64,
+                                   _P, c_int64, _P, c_int64, _P]),
     "dsa_prefill_windows": (c_int, [_P, _P, c_int, c_int, c_int, c_int, _P, _P, _P, _P]),
     "dsa_indexer_k_transform_store": (c_int, [_P, c_int64, _P, _P, c_float, _P, c_int64, _P, c_int, _P, c_int,
                                               c_int, _P, c_int, _P]),

@@ -117,10 +117,13 @@ gather_indexer_cache_kernel(const uint8_t* __restrict__ cache, int64_t page_byte
 // row: for a cached row lane l dequantises nope bytes 8l .. 8l+7 with the
 // scale of tile l/16 (exact: fp8 times a power of two is a bf16 value) and
 // writes 16 bytes; lanes 0-7 copy the 128-byte bf16 rope tail. A fresh row is
-// a 1152-byte copy in 16-byte pieces.
+// a 1152-byte copy in 16-byte pieces. A cached row whose block-table column is
+// past the table's width, or whose block is negative or past the cache, is
+// written as zeros (the row is never read).
 __global__ void __launch_bounds__(256)
-mla_prefill_kv_kernel(const uint8_t* __restrict__ cache, int64_t block_stride, int block_size,
-                      const int32_t* __restrict__ block_table, int64_t bt_stride, const void* __restrict__ cu_q,
+mla_prefill_kv_kernel(const uint8_t* __restrict__ cache, int64_t block_stride, int block_size, int64_t num_blocks,
+                      const int32_t* __restrict__ block_table, int64_t bt_stride, int bt_width,
+                      const void* __restrict__ cu_q,
                       const void* __restrict__ cu_k, int cu_is_64, int num_seqs, int64_t total_k,
                       const uint16_t* __restrict__ fresh, int64_t fresh_stride, uint16_t* __restrict__ out,
                       int64_t out_stride) {
@@ -137,7 +140,13 @@ mla_prefill_kv_kernel(const uint8_t* __restrict__ cache, int64_t block_stride, i
   const int64_t i = r - k0, cached = (k1 - k0) - (q1 - q0);
   uint8_t* dst = reinterpret_cast<uint8_t*>(out + r * out_stride);
   if (i < cached) {
-    const int64_t blk = block_table[(int64_t)lo * bt_stride + i / block_size];
+    const int64_t col = i / block_size;
+    const int64_t blk = col < bt_width ? (int64_t)block_table[(int64_t)lo * bt_stride + col] : -1;
+    if (blk < 0 || blk >= num_blocks) {
+      *reinterpret_cast<v4i*>(dst + 16 * lane) = v4i{0, 0, 0, 0};
+      if (lane < 8) *reinterpret_cast<v4i*>(dst + 1024 + 16 * lane) = v4i{0, 0, 0, 0};
+      return;
+    }
     const uint8_t* row = cache + blk * block_stride + (i % block_size) * 656;
     const uint2 codes = *reinterpret_cast<const uint2*>(row + 8 * lane);
     const float scale = reinterpret_cast<const float*>(row + 512)[lane >> 4];
@@ -212,12 +221,14 @@ int dsa_gather_indexer_cache(const uint8_t* cache, int64_t page_bytes, int page_
 }
 
 int dsa_mla_prefill_kv(const uint8_t* kv_cache, int64_t kv_block_stride_bytes, int kv_block_size,
-                       const int32_t* block_table, int64_t bt_stride, const void* cu_seqlens_q,
+                       int64_t kv_num_blocks, const int32_t* block_table, int64_t bt_stride, int bt_width,
+                       const void* cu_seqlens_q,
                        const void* cu_seqlens_k, int cu_is_64, int num_seqs, int64_t total_k, const void* fresh,
                        int64_t fresh_row_stride, void* out, int64_t out_row_stride, void* stream) {
   using namespace dsa;
   if (num_seqs < 1 || total_k < 0 || kv_block_size <= 0 || fresh_row_stride < 576 || out_row_stride < 576 ||
-      kv_block_stride_bytes < (int64_t)kv_block_size * 656)
+      kv_block_stride_bytes < (int64_t)kv_block_size * 656 || kv_num_blocks < 0 || bt_width < 0 ||
+      bt_stride < bt_width)
     return set_error(kInvalidArgument, "dsa_mla_prefill_kv: bad sizes");
   if (total_k == 0) return kOk;
   if (!kv_cache || !block_table || !cu_seqlens_q || !cu_seqlens_k || !fresh || !out)
@@ -229,7 +240,8 @@ int dsa_mla_prefill_kv(const uint8_t* kv_cache, int64_t kv_block_stride_bytes, i
   const int64_t nwg = (total_k + 3) / 4;
   if (nwg > INT32_MAX) return set_error(kInvalidArgument, "dsa_mla_prefill_kv: too many rows");
   hipLaunchKernelGGL(mla_prefill_kv_kernel, dim3((unsigned)nwg), dim3(256), 0, (hipStream_t)stream, kv_cache,
-                     kv_block_stride_bytes, kv_block_size, block_table, bt_stride, cu_seqlens_q, cu_seqlens_k,
+                     kv_block_stride_bytes, kv_block_size, kv_num_blocks, block_table, bt_stride, bt_width,
+                     cu_seqlens_q, cu_seqlens_k,
                      cu_is_64, num_seqs, total_k, static_cast<const uint16_t*>(fresh), fresh_row_stride,
                      static_cast<uint16_t*>(out), out_row_stride);
   return check_launch("dsa_mla_prefill_kv");

@@ -829,7 +829,7 @@ int dsa_sparse_mla_num_splits(int num_tokens, int num_heads, int topk, int num_c
   // keep at least 4 blocks per workgroup (below that the start-up and the
   // combine outweigh the shorter key list). Splits must divide topk into
   // 64-row blocks.
-  const int max_splits = std::min(8, topk / dsa::kMlaKeys);
+  const int max_splits = std::min(8, topk / (4 * dsa::kMlaKeys));
   int splits = 1;
   while (splits * 2 <= max_splits && base * splits * 2 <= num_cus && (topk / (splits * 2)) % dsa::kMlaKeys == 0)
     splits *= 2;

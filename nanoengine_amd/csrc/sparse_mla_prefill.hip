@@ -359,7 +359,7 @@ sparse_mla_prefill_kernel(const PrParams P) {
 __global__ void __launch_bounds__(256)
 prefill_split_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int topk, const void* __restrict__ cu_q,
                      const void* __restrict__ cu_k, int cu_is_64, int num_seqs, int64_t total_k,
-                     const int32_t* __restrict__ bt, int64_t bt_stride, int block_size,
+                     const int32_t* __restrict__ bt, int64_t bt_stride, int bt_width, int block_size,
                      int32_t* __restrict__ cached, int cached_w, int32_t* __restrict__ fresh, int fresh_w,
                      int32_t* __restrict__ counts) {
   auto cu = [&](const void* p, int i) -> int64_t {
@@ -387,8 +387,13 @@ prefill_split_kernel(const int32_t* __restrict__ idx, int64_t idx_stride, int to
       const int64_t ncached = (k1 - k0) - (cu(cu_q, lo + 1) - cu(cu_q, lo));
       const int64_t i = g - k0;
       if (i < ncached) {
-        kind = 0;
-        v = bt[(int64_t)lo * bt_stride + i / block_size] * block_size + (int32_t)(i % block_size);
+        // a block-table column past the table's width is skipped like -1; a
+        // stale or negative block gives a slot the MLA kernel skips
+        const int64_t col = i / block_size;
+        if (col < bt_width) {
+          kind = 0;
+          v = bt[(int64_t)lo * bt_stride + col] * block_size + (int32_t)(i % block_size);
+        }
       } else {
         kind = 1;
         v = (int32_t)(cu(cu_q, lo) + i - ncached);
@@ -512,13 +517,14 @@ size_t dsa_sparse_mla_prefill_paged_workspace_bytes(int num_tokens, int topk) {
 int dsa_sparse_mla_prefill_paged(const void* q, int64_t q_token_stride, int64_t q_head_stride,
                                  const uint8_t* kv_cache, int64_t kv_block_stride_bytes, int kv_block_size,
                                  int64_t kv_num_blocks, const int32_t* block_table, int64_t bt_stride,
-                                 const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64, int num_seqs,
+                                 int bt_width, const void* cu_seqlens_q, const void* cu_seqlens_k, int cu_is_64, int num_seqs,
                                  int64_t total_k, const void* fresh, int64_t fresh_row_stride, int64_t total_q,
                                  const int32_t* indices, int64_t idx_stride, int num_tokens, int num_heads, int topk,
                                  float sm_scale, void* out, float* max_logits, float* lse, void* workspace,
                                  size_t workspace_bytes, void* stream) {
   using namespace dsa;
-  if (num_tokens < 0 || num_seqs < 1 || total_k < 0 || total_q < 0 || topk <= 0 || kv_block_size <= 0)
+  if (num_tokens < 0 || num_seqs < 1 || total_k < 0 || total_q < 0 || topk <= 0 || kv_block_size <= 0 ||
+      bt_width < 0 || bt_stride < bt_width)
     return set_error(kInvalidArgument, "sparse_mla_prefill_paged: bad sizes");
   if (num_tokens == 0) return kOk;
   if (!indices || !block_table || !cu_seqlens_q || !cu_seqlens_k || !out || !max_logits || !lse || !workspace)
@@ -535,7 +541,8 @@ int dsa_sparse_mla_prefill_paged(const void* q, int64_t q_token_stride, int64_t 
   hipStream_t st = (hipStream_t)stream;
   // 1. each token's indices split into cache slots and fresh rows, compacted and counted
   hipLaunchKernelGGL(prefill_split_kernel, dim3((unsigned)num_tokens), dim3(256), 0, st, indices, idx_stride, topk,
-                     cu_seqlens_q, cu_seqlens_k, cu_is_64, num_seqs, total_k, block_table, bt_stride, kv_block_size,
+                     cu_seqlens_q, cu_seqlens_k, cu_is_64, num_seqs, total_k, block_table, bt_stride, bt_width,
+                     kv_block_size,
                      cached, cw, fresh_idx, fw, counts);
   if (int rc = check_launch("dsa_sparse_mla_prefill_paged(split)")) return rc;
   // 2. the decode kernel over each token's cache slots (fp8 rows, exact

@@ -540,8 +540,8 @@ def mla_prefill_kv(k_cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_
     _require(out.dtype == torch.bfloat16 and tuple(out.shape) == (total_k, MLA_D_QK) and out.stride(1) == 1,
              f"out must be bf16 [{total_k}, {MLA_D_QK}]", ValueError)
     dev = _check_cuda(k_cache, block_table, cu_seqlens_q, cu_seqlens_k, fresh, out)
-    _lib.call("dsa_mla_prefill_kv", _as_bytes(k_cache).data_ptr(), blk_stride, block_size, block_table.data_ptr(),
-              block_table.stride(0), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+    _lib.call("dsa_mla_prefill_kv", _as_bytes(k_cache).data_ptr(), blk_stride, block_size, k_cache.shape[0],
+              block_table.data_ptr(), block_table.stride(0), block_table.shape[1], cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
               int(cu_seqlens_q.dtype == torch.int64), num_seqs, int(total_k), fresh.data_ptr(), fresh.stride(0),
               out.data_ptr(), out.stride(0), _stream(dev))
 
@@ -664,7 +664,8 @@ def sparse_mla_prefill_paged(q: torch.Tensor, k_cache: torch.Tensor, block_table
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
     _lib.call("dsa_sparse_mla_prefill_paged", q.data_ptr(), q.stride(0), q.stride(1), _as_bytes(k_cache).data_ptr(),
               blk_stride, block_size, k_cache.shape[0], block_table.data_ptr(), block_table.stride(0),
-              cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), int(cu_seqlens_q.dtype == torch.int64), num_seqs,
+              block_table.shape[1], cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+              int(cu_seqlens_q.dtype == torch.int64), num_seqs,
               int(total_k), f2.data_ptr(), f2.stride(0), f2.shape[0], indices.data_ptr(), indices.stride(0), T, H,
               topk, float(sm_scale), out.data_ptr(), max_logits.data_ptr(), lse.data_ptr(), workspace.data_ptr(),
               workspace.numel(), _stream(dev))

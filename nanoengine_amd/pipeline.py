@@ -9,6 +9,16 @@ once in the constructor, so a step allocates nothing (capturable in a HIP
 graph). By default the indexer and the top-k run fused (``ops.indexer_topk``:
 the logits are never written to memory); ``fused=False`` runs them as the two
 separate reference operators over a logits buffer.
+
+Buffer ownership: a call returns views of the object's own buffers (o, lse,
+logical, physical), and the next call on the same object overwrites them. A
+model that runs several layers through one object passes ``out=`` / ``lse=``
+per layer (its own [rows, H, 512] bf16 and [rows, H] f32 tensors) to keep each
+layer's attention output. The (logical, physical) pair a full layer publishes
+to an ``IndexerTopKState`` is held by reference: the next full layer on the
+same object rewrites it in place, which is also the moment the reference's
+state moves on to the new layer's selection (deepseek_v2.py:1917-1950), so the
+shared layers in between read the pair of the full layer before them.
 """
 from __future__ import annotations
 
@@ -56,7 +66,7 @@ class DsaDecodeStep:
                  seq_lens: torch.Tensor, block_tables: torch.Tensor, page_tables: torch.Tensor,
                  q_mla: torch.Tensor, kv_cache: torch.Tensor, sm_scale: float, *,
                  layer_idx: int | None = None, indexer_state: IndexerTopKState | None = None,
-                 shared: bool = False):
+                 shared: bool = False, out: torch.Tensor | None = None, lse: torch.Tensor | None = None):
         """q_idx_fp8 [B*n, 64, 128] fp8; weights [B*n, 64] f32; indexer_cache
         [pages, 8448] uint8; seq_lens [B*n] int32 per-query lengths;
         block_tables [B, M] int32; page_tables [B*n, M] int32 (block_tables
@@ -67,15 +77,19 @@ class DsaDecodeStep:
         (logical, physical) pair under ``layer_idx``; a shared layer
         (``shared=True``) runs no indexer and attends over the published pair,
         which must match this batch's shape (deepseek_v2.py:1865-1950). The
-        indexer inputs are not read on a shared layer and may be None."""
+        indexer inputs are not read on a shared layer and may be None.
+        ``out`` [B*n, H, 512] bf16 and ``lse`` [B*n, H] f32, when given, receive
+        this call's attention output instead of the object's own buffers."""
+        o_buf = self.out if out is None else out
+        lse_buf = self.lse if lse is None else lse
         if shared:
             if indexer_state is None:
                 raise ValueError("a shared indexer layer needs the indexer_state of a preceding full layer")
             logical, physical = indexer_state.require(layer_idx, self.batch * self.next_n, self.topk,
                                                       require_physical=True)
-            ops.sparse_mla_decode(q_mla, kv_cache, physical, sm_scale, out=self.out, lse=self.lse,
+            ops.sparse_mla_decode(q_mla, kv_cache, physical, sm_scale, out=o_buf, lse=lse_buf,
                                   num_splits=self.num_splits, workspace=self.workspace)
-            return self.out, self.lse, logical, physical
+            return o_buf, lse_buf, logical, physical
         B, n = self.batch, self.next_n
         q4 = q_idx_fp8.view(B, n, *q_idx_fp8.shape[1:])
         if self.fused:
@@ -88,6 +102,6 @@ class DsaDecodeStep:
                                self.logical, workspace=self.topk_workspace)
         if indexer_state is not None:
             indexer_state.publish(layer_idx, self.logical, self.physical)
-        ops.sparse_mla_decode(q_mla, kv_cache, self.physical, sm_scale, out=self.out, lse=self.lse,
+        ops.sparse_mla_decode(q_mla, kv_cache, self.physical, sm_scale, out=o_buf, lse=lse_buf,
                               num_splits=self.num_splits, workspace=self.workspace)
-        return self.out, self.lse, self.logical, self.physical
+        return o_buf, lse_buf, self.logical, self.physical

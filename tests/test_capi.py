@@ -88,7 +88,8 @@ def test_workspace_size_queries(lib):
     assert lib.dsa_sparse_mla_num_splits(32, 128, 2048, 256) == 4
     assert lib.dsa_sparse_mla_num_splits(96, 128, 2048, 256) == 1   # two rounds of workgroups cost more
     assert lib.dsa_sparse_mla_num_splits(4, 128, 2048, 256) == 8    # at least 4 blocks per workgroup
-    assert lib.dsa_sparse_mla_num_splits(1, 16, 128, 256) == 2
+    assert lib.dsa_sparse_mla_num_splits(1, 16, 128, 256) == 1      # two blocks: no split
+    assert lib.dsa_sparse_mla_num_splits(1, 16, 512, 256) == 2      # eight blocks: two splits of four
 
 
 def test_prefill_entry_points_reject_bad_arguments(lib):
@@ -97,10 +98,14 @@ def test_prefill_entry_points_reject_bad_arguments(lib):
     assert lib.dsa_prefill_windows(P, P, 0, 0, 4, 64, P, P, P, P) == 1
     assert lib.dsa_prefill_windows(P, P, 0, 2, 4, 0, P, P, P, P) == 1
     assert b"null pointer" in (lib.dsa_prefill_windows(P, P, 0, 2, 4, 64, P, P, P, P) == 1 and lib.dsa_last_error())
-    # key assembly: rows of 576, a block stride that holds the block's rows, 16-byte alignment
-    assert lib.dsa_mla_prefill_kv(P, 64 * 656 - 1, 64, P, 0, P, P, 0, 1, 10, P, 576, P, 576, P) == 1
-    assert lib.dsa_mla_prefill_kv(P, 42640, 64, P, 0, P, P, 0, 1, 10, P, 512, P, 576, P) == 1
-    assert lib.dsa_mla_prefill_kv(P, 42640, 64, P, 0, P, P, 0, 1, 0, P, 576, P, 576, P) == 0   # nothing to do
+    # key assembly: rows of 576, a block stride that holds the block's rows, a
+    # block count and table width that are not negative, 16-byte alignment
+    assert lib.dsa_mla_prefill_kv(P, 64 * 656 - 1, 64, 8, P, 4, 4, P, P, 0, 1, 10, P, 576, P, 576, P) == 1
+    assert lib.dsa_mla_prefill_kv(P, 42640, 64, 8, P, 4, 4, P, P, 0, 1, 10, P, 512, P, 576, P) == 1
+    assert lib.dsa_mla_prefill_kv(P, 42640, 64, -1, P, 4, 4, P, P, 0, 1, 10, P, 576, P, 576, P) == 1
+    assert lib.dsa_mla_prefill_kv(P, 42640, 64, 8, P, 4, -1, P, P, 0, 1, 10, P, 576, P, 576, P) == 1
+    assert lib.dsa_mla_prefill_kv(P, 42640, 64, 8, P, 3, 4, P, P, 0, 1, 10, P, 576, P, 576, P) == 1   # stride < width
+    assert lib.dsa_mla_prefill_kv(P, 42640, 64, 8, P, 4, 4, P, P, 0, 1, 0, P, 576, P, 576, P) == 0   # nothing to do
     # paged sparse prefill: workspace sizing and the workspace check come before any launch
     # cache-slot and fresh-row lists, 2048 wide each, and two counts per token
     assert lib.dsa_sparse_mla_prefill_paged_workspace_bytes(8192, 2048) == 2 * 8192 * 2048 * 4 + 8192 * 8
@@ -108,15 +113,18 @@ def test_prefill_entry_points_reject_bad_arguments(lib):
     ws = lib.dsa_sparse_mla_prefill_paged_workspace_bytes(10, 2048)
     f = ctypes.c_float(0.1)
     one = ctypes.c_void_p(16)  # a non-null address that is never dereferenced
-    args = [one, 0, 0, one, 42640, 64, 10, one, 0, one, one, 0, 1, 100, one, 576, 10, one, 2048, 10, 128, 2048,
+    args = [one, 0, 0, one, 42640, 64, 10, one, 4, 4, one, one, 0, 1, 100, one, 576, 10, one, 2048, 10, 128, 2048,
             f, one, one, one, one]
     assert lib.dsa_sparse_mla_prefill_paged(*args, ws - 1, P) == 4          # workspace too small
     assert b"workspace" in lib.dsa_last_error()
     bad = list(args)
-    bad[12] = 0                                                             # no sequences
+    bad[13] = 0                                                             # no sequences
     assert lib.dsa_sparse_mla_prefill_paged(*bad, ws, P) == 1
     bad = list(args)
-    bad[26] = P                                                             # no workspace
+    bad[27] = P                                                             # no workspace
+    assert lib.dsa_sparse_mla_prefill_paged(*bad, ws, P) == 1
+    bad = list(args)
+    bad[9] = 5                                                              # table width > row stride
     assert lib.dsa_sparse_mla_prefill_paged(*bad, ws, P) == 1
 
 

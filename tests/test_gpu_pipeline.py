@@ -108,3 +108,45 @@ def test_shared_layer_reuses_the_published_topk(cuda):
     small.publish(2, published[0][:2], published[1][:2])
     with pytest.raises(RuntimeError, match="stale TopK shape"):
         step(None, None, None, None, None, None, q3, kv3, 0.1, layer_idx=3, indexer_state=small, shared=True)
+
+
+def test_full_shared_full_layers_keep_each_output(cuda):
+    """Layers 0 (full), 1 (shared) and 2 (full) of one step. Layers 0 and 2
+    run through step object A with their own out=/lse= tensors; layer 1
+    runs through a second object B over A's published pair. After layer 2,
+    every layer's output still equals sparse MLA over the selection it used
+    (layer 0's pair for layers 0 and 1, layer 2's own for layer 2), and the
+    state has moved on to layer 2's pair."""
+    from nanoengine_amd import ops
+    from nanoengine_amd.state import IndexerTopKState
+    lens, n, H = [3000, 20000, 700, 9000], 1, 128
+    inp, kv, q, max_ctx = _step_inputs(lens, n, H, seed=31)
+    B = len(lens)
+    A = DsaDecodeStep(B, n, max_ctx, num_heads=H, device=cuda)
+    Bs = DsaDecodeStep(B, n, max_ctx, num_heads=H, device=cuda)
+    state = IndexerTopKState()
+    seq = A.expand_lens(inp.context_lens)
+    layers = []
+    for i in range(3):
+        layers.append((synth.make_mla_query(B * n, H, seed=100 + i, device="cuda"),
+                       synth.make_mla_cache(kv.shape[0], seed=100 + i, device="cuda")))
+    outs = [(torch.empty(B * n, H, 512, dtype=torch.bfloat16, device=cuda),
+             torch.empty(B * n, H, dtype=torch.float32, device=cuda)) for _ in range(3)]
+    # layer 2's indexer sees another query, so it selects differently
+    q_idx2 = synth.make_indexer_inputs(lens, next_n=n, seed=32, device=cuda).q_fp8
+    _, _, lg0, ph0 = A(inp.q_fp8, inp.weights, inp.cache, seq, inp.block_tables, inp.block_tables, *layers[0],
+                       192 ** -0.5, layer_idx=0, indexer_state=state, out=outs[0][0], lse=outs[0][1])
+    sel0 = ph0.clone()
+    o1, l1, _, ph1 = Bs(None, None, None, None, None, None, *layers[1], 192 ** -0.5, layer_idx=1,
+                        indexer_state=state, shared=True, out=outs[1][0], lse=outs[1][1])
+    assert o1 is outs[1][0] and l1 is outs[1][1] and ph1 is ph0
+    A(q_idx2, inp.weights, inp.cache, seq, inp.block_tables, inp.block_tables, *layers[2], 192 ** -0.5,
+      layer_idx=2, indexer_state=state, out=outs[2][0], lse=outs[2][1])
+    sel2 = A.physical.clone()
+    torch.cuda.synchronize()
+    assert not torch.equal(sel0, sel2), "layer 2 should select other slots"
+    assert state.source_layer == 2 and state.physical_indices is A.physical
+    for i, sel in ((0, sel0), (1, sel0), (2, sel2)):
+        eo, el = ops.sparse_mla_decode(layers[i][0], layers[i][1], sel, 192 ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[i][0], eo) and torch.equal(outs[i][1], el), f"layer {i}"

@@ -127,3 +127,43 @@ def test_flash_mla_sparse_fwd_paged_adapter(cuda):
     assert torch.equal(torch.nan_to_num(mx, neginf=-1e30), torch.nan_to_num(mx2, neginf=-1e30))
     with pytest.raises(ValueError):
         flash_mla.flash_mla_sparse_fwd_paged(q, kv, bt, cu_q, cu_k, fresh, idx, scale)   # indices not [s_q, 1, topk]
+
+
+def test_bad_block_table_entries_are_skipped(cuda):
+    """Block-table entries that point outside the cache (-1, past the block
+    count) or columns past the table's width: the key assembly writes those
+    cached rows as zeros, and the paged sparse prefill skips them like an
+    index of -1. The table is passed as a narrowed view (row stride 63,
+    width 40), so sequence 4's cached rows from 2560 on lie past its width."""
+    print("prefill bad block-table entries", flush=True)
+    q, kv, bt, cu_q, cu_k, fresh, idx, total_k, host = _paged_case(cuda, seed=13)
+    bt_h, cu_q_h, cu_k_h, idx_h = host
+    nblk = kv.shape[0]
+    bad_bt = bt_h.copy()
+    bad_bt[3, 2] = -1
+    bad_bt[3, 5] = nblk + 7
+    W = 40
+    bt_view = torch.from_numpy(bad_bt).to(cuda)[:, :W]
+    assert bt_view.stride(0) == bt_h.shape[1] and bt_view.shape[1] == W
+    # which ragged key rows are unusable
+    bad_row = np.zeros(total_k, bool)
+    for b in range(len(cu_q_h) - 1):
+        cached = (cu_k_h[b + 1] - cu_k_h[b]) - (cu_q_h[b + 1] - cu_q_h[b])
+        for i in range(cached):
+            col = i // 64
+            bad_row[cu_k_h[b] + i] = col >= W or not (0 <= bad_bt[b, col] < nblk)
+    assert bad_row.sum() > 1000
+    rows = kv.contiguous().reshape(-1, 656).cpu().numpy()
+    exp = O.assemble_prefill_kv(rows, 64, bt_h, cu_q_h, cu_k_h, fresh.float().cpu().numpy())
+    exp[bad_row] = 0.0
+    out = torch.empty(total_k, 576, dtype=torch.bfloat16, device=cuda)
+    ops.mla_prefill_kv(kv, bt_view, cu_q, cu_k, fresh, total_k, out)
+    scale = 192 ** -0.5
+    o, mx, lse = ops.sparse_mla_prefill_paged(q, kv, bt_view, cu_q, cu_k, fresh, idx, scale, total_k)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.float().cpu().numpy(), exp)
+    idx_skip = np.where((idx_h >= 0) & (idx_h < total_k) & bad_row[np.clip(idx_h, 0, total_k - 1)], -1, idx_h)
+    sample = np.array([int(cu_q_h[3]), int(cu_q_h[3]) + 30, int(cu_q_h[4]), int(cu_q_h[4]) + 2, 0, 50])
+    oo, omx, olse = O.sparse_mla_prefill(q[sample].float().cpu().numpy(), exp, idx_skip[sample], scale)
+    assert np.abs(o[sample].float().cpu().numpy() - oo).max() <= 2e-2
+    assert np.abs(lse[sample].cpu().numpy() - olse).max() <= 1e-3
