@@ -814,15 +814,16 @@ def decode_line(args, config: int) -> dict | None:
         run()
     torch.cuda.synchronize()
     # Per-phase durations with HIP events on the launch stream, in a pass of
-    # its own before the wall-timed loop. It runs at least 100 steps: the GPU
-    # clock ramps over the first ~100 steps of load (325 -> 305 us/step at
-    # config 2), so this pass also hands the wall loop a settled clock.
-    ev_steps = max(args.steps, 100)
+    # its own before the wall-timed loop. It runs at least 300 steps (~0.1 s):
+    # the GPU clock ramps over the first ~100 steps of load (325 -> 305
+    # us/step at config 2), so this pass also hands the wall loop a settled
+    # clock, and its averages are taken over its last `steps` steps.
+    ev_steps = max(args.steps, 300)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(ev_steps)]
     for e in evs:
         run(e)
     torch.cuda.synchronize()
-    ph = [[e[i].elapsed_time(e[i + 1]) * 1e3 for e in evs] for i in range(4)]   # us
+    ph = [[e[i].elapsed_time(e[i + 1]) * 1e3 for e in evs[-args.steps:]] for i in range(4)]   # us
     med = [sorted(x)[len(x) // 2] for x in ph]
     avg = [sum(x) / len(x) for x in ph]
     idx_total = sum(avg[0:3])
