@@ -954,13 +954,15 @@ def main():
                 print(f"bench: config {cfg}", file=sys.stderr, flush=True)
                 line["other_configs"][f"config{cfg}"] = _summary(fn(other))
                 _free_gpu()
-            bad = [k for k, v in line["other_configs"].items() if not (v.get("parity") or {}).get("ok", False)]
-            line["other_configs_parity_ok"] = not bad
+            # None: some config ran without its check (--no-cpu-baseline)
+            checked = [v["parity"]["ok"] for v in line["other_configs"].values() if v.get("parity") is not None]
+            line["other_configs_parity_ok"] = all(checked) if len(checked) == 3 else (False if not all(checked) else None)
     if line is None:   # a --only profiling run
         return
     print(json.dumps(line), flush=True)
     failed = [] if (line.get("parity") or {"ok": True})["ok"] else ["headline"]
-    failed += [k for k, v in line.get("other_configs", {}).items() if not (v.get("parity") or {}).get("ok", False)]
+    failed += [k for k, v in line.get("other_configs", {}).items()
+               if v.get("parity") is not None and not v["parity"]["ok"]]
     if failed:
         print(f"PARITY FAILURE in {failed}: the GPU outputs do not match the oracle", file=sys.stderr)
         sys.exit(1)
