@@ -3,10 +3,12 @@
 //   logits[b*n+j, t] = sum_h w[b*n+j, h] * relu(q[b,j,h,:] . k[t,:]) * scale[t]
 //
 // One wave owns one 64-token page at a time. The page's 64x128 fp8 keys are
-// loaded straight from HBM into registers as the B operand of
-// v_mfma_scale_f32_16x16x128_f8f6f4 (fp8 x fp8 -> fp32, unit scales), 32
-// contiguous bytes per lane, while the query heads (A operand, 16 heads per
-// tile) stay resident in registers for the whole workgroup lifetime. Each page
+// the B operand of v_mfma_scale_f32_16x16x128_f8f6f4 (fp8 x fp8 -> fp32, unit
+// scales), 32 contiguous bytes of one token per lane, while the query heads
+// (A operand, 16 heads per tile) stay resident in registers for the whole
+// workgroup lifetime. indexer_logits_kernel loads the keys from HBM straight
+// into that layout; the persistent filter pass loads whole 128-byte rows per
+// instruction and reorders them through a per-wave LDS tile. Each page
 // costs 16 MFMAs per query token (4 token tiles x 4 head tiles); the ReLU and
 // the head weights are applied on the fp32 accumulators, and a 3-shuffle
 // butterfly finishes the head sum so that lane l ends up owning token l of the
@@ -349,9 +351,11 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
 // workgroups per CU) where each wave streams one contiguous, balanced range
 // of the flattened (batch entry, page) space through its rotating page
 // buffers, with no barriers and no per-workgroup start-up or drain in the
-// loop. Candidates are staged per wave in LDS (wave-uniform counters, no LDS
-// atomics) and flushed to the row's list with one global atomic when the
-// batch entry changes, when the stage could overflow, and at the end.
+// loop. Pages are read as whole rows (load_page_rows) and reordered into the
+// MFMA operand layout in the wave's LDS tile (rows_to_operands). Candidates
+// are staged per wave in LDS (wave-uniform counters, no LDS atomics) and
+// flushed to the row's list with one global atomic when the batch entry
+// changes, when the stage could overflow, and at the end.
 constexpr int kFiltStageCap = 384;   // staged candidates per wave and query token
 constexpr int kFiltWindow = 64;      // block-table entries a wave holds (one per lane)
 constexpr int kFiltAdvance = 60;     // pages per window refill (a multiple of the 3- and 4-buffer rotations)
@@ -359,6 +363,7 @@ constexpr int kFiltMaxBatch = 8192;  // batch entries whose page prefix fits in 
 struct FiltWaveStage {
   uint32_t key[2][kFiltStageCap];
   uint32_t pos[2][kFiltStageCap];
+  __attribute__((aligned(16))) uint8_t tr[kIdxTrBytes];  // the wave's page tile (rows_to_operands)
 };
 constexpr size_t filt_smem_bytes(int batch) {
   return sizeof(FiltWaveStage) * kIdxWaves + ((size_t)batch + 1 + kIdxWaves) * sizeof(int32_t);
@@ -483,7 +488,8 @@ indexer_filter_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
   auto page_ptr = [&](int k) {
     return kv + (int64_t)__builtin_amdgcn_readlane(win_page, k - wb) * kIdxPageBytes;
   };
-  auto compute = [&](const PageRegs& pr, int k) {
+  auto compute = [&](PageRegs& pr, int k) {
+    rows_to_operands(pr, st.tr, lane);
     const int b = __builtin_amdgcn_readlane(win_b, k - wb);
     if (b != cur_b) enter(b);
     const int page = (int)(p0 + k - prefix[b]);
@@ -510,11 +516,11 @@ indexer_filter_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
   PageRegs buf[NB];
 #pragma unroll
   for (int u = 0; u < NB - 1; ++u)
-    if (u < n) load_page(buf[u], page_ptr(u), lane);
+    if (u < n) load_page_rows(buf[u], page_ptr(u), lane);
   for (int k = 0; k < n; k += NB) {
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-      if (k + u + NB - 1 < n) load_page(buf[(u + NB - 1) % NB], page_ptr(k + u + NB - 1), lane);
+      if (k + u + NB - 1 < n) load_page_rows(buf[(u + NB - 1) % NB], page_ptr(k + u + NB - 1), lane);
       if (k + u < n) compute(buf[u], k + u);
     }
     if (k + NB - wb == kFiltAdvance) {

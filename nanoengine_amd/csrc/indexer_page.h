@@ -50,6 +50,50 @@ __device__ __forceinline__ void load_page(PageRegs& pr, const uint8_t* page, int
   pr.scale = __builtin_nontemporal_load(reinterpret_cast<const float*>(page + kIdxPageTokens * kIdxHeadDim) + lane);
 }
 
+// A page as whole 128-byte rows per load instruction (nontemporal): chunk
+// c = 2tt + h of the page (1 KB = rows 8c .. 8c+7) goes to pr.k[tt] dwords
+// 4h .. 4h+3, lane l holding row 8c + l/8, bytes 16(l%8) .. +16. A load
+// instruction of load_page touches 16 rows (half of each 128-byte line);
+// one of these touches 8 whole rows, and the persistent filter pass reads
+// its 1.1 GB ~12% faster this way. rows_to_operands turns the rows into
+// load_page's operand layout through the wave's LDS tile.
+constexpr int kIdxTrRow = 144;                                  // padded row stride of the tile
+constexpr int kIdxTrBytes = kIdxPageTokens * kIdxTrRow;         // 9216 B per wave
+__device__ __forceinline__ void load_page_rows(PageRegs& pr, const uint8_t* page, int lane) {
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const v4i a = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(page + tt * 2048 + lane * 16));
+    const v4i b = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(page + tt * 2048 + 1024 + lane * 16));
+    pr.k[tt][0] = a[0]; pr.k[tt][1] = a[1]; pr.k[tt][2] = a[2]; pr.k[tt][3] = a[3];
+    pr.k[tt][4] = b[0]; pr.k[tt][5] = b[1]; pr.k[tt][6] = b[2]; pr.k[tt][7] = b[3];
+  }
+  pr.scale = __builtin_nontemporal_load(reinterpret_cast<const float*>(page + kIdxPageTokens * kIdxHeadDim) + lane);
+}
+
+// The rows of load_page_rows -> the operand layout of load_page, through the
+// calling wave's tile tr (kIdxTrBytes, 16-byte aligned, used by this wave
+// alone). Rows are kIdxTrRow = 144 bytes apart, so the 16 rows one operand
+// read touches fall on distinct LDS banks. A wave's LDS operations complete
+// in issue order, and the compiler keeps the reads after the writes to the
+// same tile, so no barrier is needed.
+__device__ __forceinline__ void rows_to_operands(PageRegs& pr, uint8_t* tr, int lane) {
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const v4i x = {pr.k[tt][4 * h], pr.k[tt][4 * h + 1], pr.k[tt][4 * h + 2], pr.k[tt][4 * h + 3]};
+      *reinterpret_cast<v4i*>(tr + (16 * tt + 8 * h + (lane >> 3)) * kIdxTrRow + (lane & 7) * 16) = x;
+    }
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const uint8_t* src = tr + (16 * tt + (lane & 15)) * kIdxTrRow + (lane >> 4) * 32;
+    const v4i a = *reinterpret_cast<const v4i*>(src);
+    const v4i b = *reinterpret_cast<const v4i*>(src + 16);
+    pr.k[tt][0] = a[0]; pr.k[tt][1] = a[1]; pr.k[tt][2] = a[2]; pr.k[tt][3] = a[3];
+    pr.k[tt][4] = b[0]; pr.k[tt][5] = b[1]; pr.k[tt][6] = b[2]; pr.k[tt][7] = b[3];
+  }
+}
+
 // Query token j's heads as MFMA A operands (tile ht row i = head ht*16 + i)
 // and this lane's head weights (head ht*16 + (lane/16)*4 + r).
 __device__ __forceinline__ void load_query(const uint8_t* q_row, const float* w_row, int lane, v8i (&qa)[4],
