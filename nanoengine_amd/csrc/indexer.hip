@@ -54,8 +54,8 @@ struct IdxOut {
 
 constexpr int kIdxWgTokens = kIdxWaves * kIdxPagesPerWave * kIdxPageTokens;  // 1536
 
-struct IdxStageNone {
-  uint32_t unused;
+struct IdxStoreLds {  // store mode: the waves' page tiles (rows_to_operands)
+  __attribute__((aligned(16))) uint8_t tr[kIdxWaves][kIdxTrBytes];
 };
 
 constexpr int kSamplePages = 16;  // sampled pages per row, one workgroup
@@ -82,6 +82,7 @@ struct IdxStage {  // per-WG LDS staging of kIdxFilter candidates, per query tok
   uint32_t base[2];
   uint32_t key[2][kIdxWgTokens];
   uint32_t pos[2][kIdxWgTokens];
+  __attribute__((aligned(16))) uint8_t tr[kIdxWaves][kIdxTrBytes];  // the waves' page tiles
 };
 
 template <int NQ, int MODE>
@@ -133,7 +134,7 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
   // LDS: candidate staging (filter) or the sampled logits (sample)
   __shared__ __align__(16) typename std::conditional<
       MODE == kIdxFilter, IdxStage,
-      typename std::conditional<MODE == kIdxSample, IdxSampleLds, IdxStageNone>::type>::type lds_mem;
+      typename std::conditional<MODE == kIdxSample, IdxSampleLds, IdxStoreLds>::type>::type lds_mem;
   IdxStage* stage = reinterpret_cast<IdxStage*>(&lds_mem);
   constexpr int NT = idx_threads<NQ, MODE>();
   constexpr int NW = NT / 64;
@@ -217,16 +218,22 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
     for (int i = 0; i < PPW; ++i)
       if (valid(i)) compute(pb[i], i);
   } else {
-    if (valid(0)) load_page(buf0, page_ptr(0), lane);
-    if (valid(1)) load_page(buf1, page_ptr(1), lane);
+    // whole-row loads, reordered in the wave's LDS tile before each page's MFMAs
+    uint8_t* tr = MODE == kIdxFilter ? stage->tr[wave] : reinterpret_cast<IdxStoreLds*>(&lds_mem)->tr[wave];
+    auto compute_rows = [&](PageRegs& pr, int i) {
+      rows_to_operands(pr, tr, lane);
+      compute(pr, i);
+    };
+    if (valid(0)) load_page_rows(buf0, page_ptr(0), lane);
+    if (valid(1)) load_page_rows(buf1, page_ptr(1), lane);
 #pragma unroll
     for (int i = 0; i < PPW; i += 3) {
-      if (valid(i + 2)) load_page(buf2, page_ptr(i + 2), lane);
-      if (valid(i)) compute(buf0, i);
-      if (valid(i + 3)) load_page(buf0, page_ptr(i + 3), lane);
-      if (valid(i + 1)) compute(buf1, i + 1);
-      if (valid(i + 4)) load_page(buf1, page_ptr(i + 4), lane);
-      if (valid(i + 2)) compute(buf2, i + 2);
+      if (valid(i + 2)) load_page_rows(buf2, page_ptr(i + 2), lane);
+      if (valid(i)) compute_rows(buf0, i);
+      if (valid(i + 3)) load_page_rows(buf0, page_ptr(i + 3), lane);
+      if (valid(i + 1)) compute_rows(buf1, i + 1);
+      if (valid(i + 4)) load_page_rows(buf1, page_ptr(i + 4), lane);
+      if (valid(i + 2)) compute_rows(buf2, i + 2);
     }
   }
 
