@@ -366,7 +366,7 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
 constexpr int kFiltStageCap = 384;   // staged candidates per wave and query token
 constexpr int kFiltWindow = 64;      // block-table entries a wave holds (one per lane)
 constexpr int kFiltAdvance = 60;     // pages per window refill (a multiple of the 3- and 4-buffer rotations)
-constexpr int kFiltMaxBatch = 8192;  // batch entries whose page prefix fits in LDS
+constexpr int kFiltMaxBatch = 4096;  // batch entries whose page prefix fits in LDS beside a second workgroup's
 struct FiltWaveStage {
   uint32_t key[2][kFiltStageCap];
   uint32_t pos[2][kFiltStageCap];
@@ -375,6 +375,7 @@ struct FiltWaveStage {
 constexpr size_t filt_smem_bytes(int batch) {
   return sizeof(FiltWaveStage) * kIdxWaves + ((size_t)batch + 1 + kIdxWaves) * sizeof(int32_t);
 }
+static_assert(2 * filt_smem_bytes(kFiltMaxBatch) <= 160 * 1024, "two filter workgroups per CU at the largest batch");
 
 template <int NQ>
 __global__ void __launch_bounds__(kIdxThreads) __attribute__((amdgpu_waves_per_eu(2)))

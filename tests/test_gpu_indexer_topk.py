@@ -94,8 +94,9 @@ def test_workspace_and_argument_checks(cuda):
 
 
 def test_fused_large_batch_takes_the_per_workgroup_filter(cuda):
-    """Batches above 8192 entries do not fit the persistent filter pass's LDS
-    page prefix and take the one-workgroup-per-24-pages filter instead; the
+    """Batches above 4096 entries do not fit the persistent filter pass's LDS
+    page prefix (two workgroups per CU) and take the one-workgroup-per-24-pages
+    filter instead; the
     selection is still exactly topk_transform over indexer_logits."""
     B, L, k = 8200, 2100, 2048
     print(f"fused large batch B={B} L={L}", flush=True)
