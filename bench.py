@@ -124,11 +124,15 @@ def micro():
     pool = torch.randint(0, 255, (npages * 8448,), dtype=torch.uint8, device=dev, generator=g)
     ids = torch.randperm(npages, device=dev, generator=g).to(torch.int32)
     per_wave = npages // (grid * 4)
-    t = timed(lambda: check(lib.dsa_mb_page_read(ctypes.c_void_p(pool.data_ptr()), ctypes.c_void_p(ids.data_ptr()),
-                                                 per_wave, grid, ctypes.c_void_p(sink.data_ptr()), st), "page_read"))
     nbytes = npages * 8448
-    print(json.dumps({"micro": "page_read", "pages": npages, "page_bytes": 8448, "waves": grid * 4,
-                      "us": round(t * 1e6, 1), "TBps": round(nbytes / t / 1e12, 3)}), flush=True)
+    for layout, name in ((0, "whole rows, plain loads"), (1, "whole rows, nontemporal loads"),
+                         (2, "MFMA operand layout, nontemporal loads")):
+        t = timed(lambda: check(lib.dsa_mb_page_read_layout(ctypes.c_void_p(pool.data_ptr()),
+                                                            ctypes.c_void_p(ids.data_ptr()), per_wave, grid, layout,
+                                                            ctypes.c_void_p(sink.data_ptr()), st), "page_read"))
+        print(json.dumps({"micro": "page_read", "layout": name, "pages": npages, "page_bytes": 8448,
+                          "waves": grid * 4, "us": round(t * 1e6, 1), "TBps": round(nbytes / t / 1e12, 3)}),
+              flush=True)
     del pool, ids
     # 2. random 656-byte rows into LDS (5 GB pool, 64-row blocks, two in flight)
     nrows, nblk, grid = (5 << 30) // 656, 32, 256

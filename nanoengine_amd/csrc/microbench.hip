@@ -2,9 +2,10 @@
 // Not part of the product library: built as libdsa_microbench.so and run by
 // `python bench.py --micro`, which prints one JSON line per measurement.
 //
-//   page_read      random 8448-byte indexer pages read with coalesced 16-byte
-//                  loads (the filter pass's access pattern): the HBM read
-//                  ceiling of that pattern;
+//   page_read      random 8448-byte indexer pages read with 16-byte loads
+//                  (the filter pass's access pattern): the HBM read ceiling
+//                  of that pattern, for plain and nontemporal whole-row loads
+//                  and for nontemporal loads in the MFMA operand layout;
 //   row_gather     random 656-byte MLA rows copied into LDS with
 //                  global_load_lds_dwordx4, 41 loads per 64-row block, two
 //                  blocks in flight (the sparse MLA gather): its ceiling;
@@ -40,7 +41,12 @@ constexpr int kRowBytes = 656;
 constexpr int kBlockBytes = 64 * kRowBytes;  // 41984 = 41 wave-wide 16-byte loads
 
 // Each wave reads pages page_ids[w * per_wave .. +per_wave) (per_wave <= 64)
-// in full, two pages in flight, the ids loaded up front.
+// in full, two pages in flight, the ids loaded up front. kLayout 0: plain
+// 16-byte loads, 1 KB contiguous per instruction (8 whole 128-byte rows);
+// 1: the same with nontemporal loads; 2: nontemporal loads in the fp8 MFMA
+// B-operand layout of the indexer (lane l: row 16t + l%16, bytes 32(l/16) +
+// 16h .. +16 of tile t and half h), each instruction touching half of 16 rows.
+template <int kLayout>
 __global__ void __launch_bounds__(256) page_read_kernel(const uint8_t* __restrict__ pool,
                                                         const int32_t* __restrict__ page_ids, int per_wave,
                                                         int* __restrict__ sink) {
@@ -52,8 +58,11 @@ __global__ void __launch_bounds__(256) page_read_kernel(const uint8_t* __restric
     const uint8_t* page = pool + (int64_t)__builtin_amdgcn_readlane(my_id, i) * kPageBytes;
 #pragma unroll
     for (int u = 0; u < 9; ++u) {
-      const int off = (u * 64 + lane) * 16;
-      x[u] = off < kPageBytes ? *reinterpret_cast<const v4i*>(page + off) : v4i{0, 0, 0, 0};
+      int off = (u * 64 + lane) * 16;
+      if (kLayout == 2 && u < 8) off = ((u >> 1) * 16 + (lane & 15)) * 128 + (lane >> 4) * 32 + (u & 1) * 16;
+      const v4i* src = reinterpret_cast<const v4i*>(page + off);
+      if (off < kPageBytes) x[u] = kLayout == 0 ? *src : __builtin_nontemporal_load(src);
+      else x[u] = v4i{0, 0, 0, 0};
     }
   };
   v4i x0[9], x1[9];
@@ -346,8 +355,24 @@ __global__ void __launch_bounds__(512) mix_kernel(int mode, int iters, float c, 
 extern "C" {
 
 MB_API int dsa_mb_page_read(const void* pool, const int32_t* page_ids, int per_wave, int grid, int* sink, void* stream) {
-  hipLaunchKernelGGL(page_read_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(page_read_kernel<0>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      static_cast<const uint8_t*>(pool), page_ids, per_wave, sink);
+  return (int)hipGetLastError();
+}
+
+// layout 0: plain whole-row loads; 1: nontemporal whole-row loads; 2: nontemporal
+// loads in the MFMA operand layout (see page_read_kernel).
+MB_API int dsa_mb_page_read_layout(const void* pool, const int32_t* page_ids, int per_wave, int grid, int layout,
+                                   int* sink, void* stream) {
+  const uint8_t* p = static_cast<const uint8_t*>(pool);
+  if (layout == 0)
+    hipLaunchKernelGGL(page_read_kernel<0>, dim3(grid), dim3(256), 0, (hipStream_t)stream, p, page_ids, per_wave, sink);
+  else if (layout == 1)
+    hipLaunchKernelGGL(page_read_kernel<1>, dim3(grid), dim3(256), 0, (hipStream_t)stream, p, page_ids, per_wave, sink);
+  else if (layout == 2)
+    hipLaunchKernelGGL(page_read_kernel<2>, dim3(grid), dim3(256), 0, (hipStream_t)stream, p, page_ids, per_wave, sink);
+  else
+    return (int)hipErrorInvalidValue;
   return (int)hipGetLastError();
 }
 

@@ -160,6 +160,6 @@ def test_microbenchmark_library_exports_its_probes():
         from nanoengine_amd import build
         build.build()
     mb = ctypes.CDLL(str(MICROBENCH_LIB))
-    for name in ["dsa_mb_page_read", "dsa_mb_row_gather", "dsa_mb_lds_read", "dsa_mb_valu_issue",
+    for name in ["dsa_mb_page_read", "dsa_mb_page_read_layout", "dsa_mb_row_gather", "dsa_mb_lds_read", "dsa_mb_valu_issue",
                  "dsa_mb_mfma_rate", "dsa_mb_mix", "dsa_mb_fp8_mfma_sum"]:
         assert hasattr(mb, name), name
