@@ -195,23 +195,33 @@ indexer_logits_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__
     compute_page<NQ, MODE>(pr, vp * step, vp, lane, qa, w, L, tk, max_ctx, o, &lds_mem, b);
   };
   if constexpr (MODE == kIdxSample) {
-    // a latency-bound pass (one workgroup per row): all of a wave's pages in
-    // flight at once
+    // A latency-bound pass (one workgroup per row). The row's query and head
+    // weights are read once per workgroup and staged in LDS, not once per
+    // wave: 16 copies of the query would double the pass's bytes. They are
+    // requested before the pages, so that waiting for them (loads complete
+    // in order) does not wait for the pages too; then all of a wave's pages
+    // go in flight at once, and the query reaches LDS while they load.
+    constexpr int kQBytes = NQ * kIdxHeads * kIdxHeadDim;
+    constexpr int kQPer = (kQBytes + 16 * NT - 1) / (16 * NT);
+    const uint8_t* qsrc = q + ((int64_t)b * NQ * kIdxHeads) * kIdxHeadDim;
+    v4i qv[kQPer];
+#pragma unroll
+    for (int u = 0; u < kQPer; ++u) {
+      const int e = 16 * ((int)threadIdx.x + u * NT);
+      if (e < kQBytes) qv[u] = *reinterpret_cast<const v4i*>(qsrc + e);
+    }
+    const float wv = threadIdx.x < NQ * kIdxHeads ? weights[(int64_t)b * NQ * kIdxHeads + threadIdx.x] : 0.f;
     PageRegs pb[PPW];
 #pragma unroll
     for (int i = 0; i < PPW; ++i)
       if (valid(i)) load_page(pb[i], page_ptr(i), lane);
-    // The row's query and head weights are read from L2 once per workgroup
-    // and staged in LDS, not once per wave: this pass is bound by each CU's
-    // read rate, and 16 copies of the query would double its bytes.
     IdxSampleLds& sq = *reinterpret_cast<IdxSampleLds*>(&lds_mem);
-    {
-      const uint8_t* qsrc = q + ((int64_t)b * NQ * kIdxHeads) * kIdxHeadDim;
-      for (int e = 16 * (int)threadIdx.x; e < NQ * kIdxHeads * kIdxHeadDim; e += 16 * NT)
-        *reinterpret_cast<v4i*>(&sq.q[0][0] + e) = *reinterpret_cast<const v4i*>(qsrc + e);
-      for (int e = threadIdx.x; e < NQ * kIdxHeads; e += NT)
-        (&sq.w[0][0])[e] = weights[(int64_t)b * NQ * kIdxHeads + e];
+#pragma unroll
+    for (int u = 0; u < kQPer; ++u) {
+      const int e = 16 * ((int)threadIdx.x + u * NT);
+      if (e < kQBytes) *reinterpret_cast<v4i*>(&sq.q[0][0] + e) = qv[u];
     }
+    if (threadIdx.x < NQ * kIdxHeads) (&sq.w[0][0])[threadIdx.x] = wv;
     __syncthreads();
     load_q(&sq.q[0][0], &sq.w[0][0]);
 #pragma unroll
