@@ -114,7 +114,8 @@ DSA_API int dsa_indexer_topk(const uint8_t* q_fp8, const uint8_t* kv_cache, cons
                              size_t workspace_bytes, void* stream, void* const* phase_events);
 
 /* Workspace bytes the top-k entry points use for `batch` rows (per-row
- * threshold, counter and a 4096-entry candidate list: 32 KB + 16 B a row). */
+ * threshold, counter, flag and a 6144-entry (key, position) candidate list:
+ * 48 KB + 16 B a row). */
 DSA_API size_t dsa_topk_workspace_bytes(int batch);
 
 /* Exact top-k selection with page-table translation.

@@ -497,7 +497,7 @@ topk_finish_kernel(const RowIn in, RowWs* __restrict__ ws, const int32_t* __rest
 //      score threshold t by a two-digit radix, exactly as the threshold kernel;
 //   2. each thread counts its keys >= t; one block scan gives every thread its
 //      place in the candidate list, which goes to LDS in thread order;
-//   3. if the list holds between k and 4096 entries, the exact top-k is the
+//   3. if the list holds between k and kListCap entries, the exact top-k is the
 //      exact top-k of the list (radix levels in LDS); otherwise the levels run
 //      over the registers (the same result without any bound);
 //   4. bitmap compaction in position order and the page translation.
