@@ -526,7 +526,10 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
                                          int split) {
   const int lane = c.lane, h = c.h, c32 = c.c32, dq = c.wave - 4;
   const float* ref = reinterpret_cast<const float*>(smem + kRefOff);
-  // this wave's exponent table (V tile dq): [4 k-steps][2 h][8 u16]
+  // this wave's exponent table (V tile dq): [4 k-steps][2 h][8 u16], written
+  // as 16-bit entries and read back as 16-byte vectors through a type that
+  // may alias them (so the reads stay after the writes)
+  typedef int v4i_alias __attribute__((ext_vector_type(4), may_alias));
   uint16_t* et = reinterpret_cast<uint16_t*>(smem + kEOff) + dq * 256;
   v16f o[2][4];  // o[mt][nn][r]: head 32mt + 8(r/4) + 4h + r%4 of the workgroup, dim 128dq + 32nn + c32
 #pragma unroll
@@ -617,7 +620,7 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
         for (int nn = 0; nn < 4; ++nn) vq[0][nn] = lds_read_tr8_at(a0 + 32 * nn);
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) pq[0][mt] = *reinterpret_cast<const v4i*>(pb + mt * 4096 + lane * 16);
-        eq[0] = *reinterpret_cast<const v4i*>(et + h * 8);
+        eq[0] = *reinterpret_cast<const v4i_alias*>(et + h * 8);
       }
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -629,7 +632,7 @@ __device__ __forceinline__ void pv_waves(const MlaParams& P, uint8_t* smem, cons
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
             pq[nxt][mt] = *reinterpret_cast<const v4i*>(pb + mt * 4096 + ((ks + 1) * 64 + lane) * 16);
-          eq[nxt] = *reinterpret_cast<const v4i*>(et + ((ks + 1) * 2 + h) * 8);
+          eq[nxt] = *reinterpret_cast<const v4i_alias*>(et + ((ks + 1) * 2 + h) * 8);
         }
         const int k2 = ks >> 1;  // k-steps 0, 1: key half 0; 2, 3: key half 1
         if (fresh && ks >= 2) continue;  // a fresh block's 32 keys are k-steps 0, 1
