@@ -947,14 +947,17 @@ def main():
         line = decode_line(args, args.config)
         if args.config == 2 and not args.headline_only and not args.only:
             # the other BASELINE configs, each with its stage figures and its
-            # parity check, as extra keys of the one line; each runs with at
-            # least 20 warm-up and 20 timed steps
+            # parity check, as extra keys of the one line; the decode configs
+            # (steps of ~0.04 and ~0.17 ms) time at least 200 steps, the
+            # prefill chunk (~14 ms) at least 20, each after at least 20
+            # warm-up steps
             _free_gpu()
             import copy
-            other = copy.copy(args)
-            other.warmup, other.steps = max(args.warmup, 20), max(args.steps, 20)
             line["other_configs"] = {}
-            for cfg, fn in ((1, bench_mla_decode), (3, lambda a: decode_line(a, 3)), (4, bench_prefill)):
+            for cfg, fn, min_steps in ((1, bench_mla_decode, 200), (3, lambda a: decode_line(a, 3), 200),
+                                       (4, bench_prefill, 20)):
+                other = copy.copy(args)
+                other.warmup, other.steps = max(args.warmup, 20), max(args.steps, min_steps)
                 print(f"bench: config {cfg}", file=sys.stderr, flush=True)
                 line["other_configs"][f"config{cfg}"] = _summary(fn(other))
                 _free_gpu()
