@@ -93,6 +93,20 @@ def test_workspace_and_argument_checks(cuda):
                          2048, out, workspace=torch.empty(16, dtype=torch.uint8, device="cuda"))
 
 
+def test_fused_batch_at_the_persistent_limit(cuda):
+    """4096 entries, the largest batch the persistent filter pass takes: its
+    LDS page prefix is at its largest (two workgroups per CU), and every
+    wave's page range crosses several batch entries; the selection is still
+    exactly topk_transform over indexer_logits."""
+    B, L, k = 4096, 2100, 2048
+    print(f"fused batch at the persistent limit B={B} L={L}", flush=True)
+    inp, cl, max_ctx = _inputs([L - (i % 64) for i in range(B)], 1, seed=4096)
+    e_phys, e_logi = _unfused(inp, cl, max_ctx, k, 1)
+    g_phys, g_logi = _fused(inp, cl, max_ctx, k, 1)
+    assert np.array_equal(g_logi, e_logi)
+    assert np.array_equal(g_phys, e_phys)
+
+
 def test_fused_large_batch_takes_the_per_workgroup_filter(cuda):
     """Batches above 4096 entries do not fit the persistent filter pass's LDS
     page prefix (two workgroups per CU) and take the one-workgroup-per-24-pages
